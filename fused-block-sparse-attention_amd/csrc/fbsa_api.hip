@@ -1,0 +1,133 @@
+// C ABI layer: host-side validation, error reporting and dispatch.
+#include <stdarg.h>
+#include <stdio.h>
+#include <math.h>
+
+#include "fbsa_common.h"
+#include "fbsa_internal.h"
+
+namespace fbsa {
+
+static thread_local char g_err[1024] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char *what) {
+  if (e == hipSuccess) return FBSA_OK;
+  (void)hipGetLastError();  // clear the sticky per-thread error so later calls are not blamed
+  return fail(FBSA_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }
+
+static bool aligned(const void *p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+// Shape and layout checks shared by the attention entry points.
+static int check_attn(const fbsa_attn_desc *d, const char *fn) {
+  if (!d) return fail(FBSA_EINVAL, "%s: null descriptor", fn);
+  if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "%s: bad dtype %d", fn, d->dtype);
+  if (d->mask < FBSA_MASK_NONE || d->mask > FBSA_MASK_TOKEN_CAUSAL) return fail(FBSA_EINVAL, "%s: bad mask %d", fn, d->mask);
+  if (d->B < 1 || d->Hq < 1 || d->Hkv < 1 || d->L < 1 || d->nblk < 1 || d->kk < 1)
+    return fail(FBSA_EINVAL, "%s: sizes must be positive (B=%lld Hq=%lld Hkv=%lld L=%lld nblk=%lld kk=%lld)", fn,
+                (long long)d->B, (long long)d->Hq, (long long)d->Hkv, (long long)d->L, (long long)d->nblk, (long long)d->kk);
+  if (d->Hq % d->Hkv) return fail(FBSA_EINVAL, "%s: Hq=%lld not a multiple of Hkv=%lld", fn, (long long)d->Hq, (long long)d->Hkv);
+  if (d->bs != 16 && d->bs != 32 && d->bs != 64 && d->bs != 128)
+    return fail(FBSA_EUNSUPPORTED, "%s: block size %lld not in {16,32,64,128}", fn, (long long)d->bs);
+  if (d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256)
+    return fail(FBSA_EUNSUPPORTED, "%s: head dim %lld not in {32,64,128,256}", fn, (long long)d->D);
+  if (d->L != d->nblk * d->bs)
+    return fail(FBSA_EINVAL, "%s: L=%lld must equal nblk*bs=%lld", fn, (long long)d->L, (long long)(d->nblk * d->bs));
+  if (d->hsel != 1 && d->hsel != d->Hkv) return fail(FBSA_EINVAL, "%s: hsel=%lld must be 1 or Hkv", fn, (long long)d->hsel);
+  if (d->l_valid < 1 || d->l_valid > d->L) return fail(FBSA_EINVAL, "%s: l_valid=%lld outside [1, L]", fn, (long long)d->l_valid);
+  if (!isfinite(d->scale)) return fail(FBSA_EINVAL, "%s: scale is not finite", fn);
+  if (d->B * d->Hq * d->nblk > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "%s: B*Hq*nblk exceeds the grid limit", fn);
+  const int64_t es = esize(d->dtype);
+  const int64_t *st[4] = {d->sq, d->sk, d->sv, d->so};
+  const char *nm[4] = {"q", "k", "v", "o"};
+  for (int t = 0; t < 4; ++t)
+    for (int x = 0; x < 3; ++x)
+      if (st[t][x] < 0 || (st[t][x] * es) % 16)
+        return fail(FBSA_EINVAL, "%s: %s stride[%d]=%lld must be a non-negative multiple of 16 bytes", fn, nm[t], x,
+                    (long long)st[t][x]);
+  return FBSA_OK;
+}
+
+static void fill_fwd(const fbsa_attn_desc *d, FwdArgs &a) {
+  a.B = d->B; a.Hq = d->Hq; a.Hkv = d->Hkv; a.L = d->L; a.nblk = d->nblk; a.kk = d->kk; a.hsel = d->hsel;
+  a.l_valid = d->l_valid;
+  for (int x = 0; x < 3; ++x) {
+    a.sq[x] = d->sq[x]; a.sk[x] = d->sk[x]; a.sv[x] = d->sv[x]; a.so[x] = d->so[x]; a.sog[x] = d->sog[x];
+  }
+  a.scale2 = d->scale * kLog2e;
+  a.mask = d->mask;
+  a.grp = (int)(d->Hq / d->Hkv);
+}
+
+}  // namespace fbsa
+
+using namespace fbsa;
+
+extern "C" {
+
+const char *fbsa_last_error(void) { return g_err; }
+
+int fbsa_version(void) { return 1; }
+
+int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const int32_t *sel,
+             const float *gate, const void *out_gate, void *o, float *lse, void *stream) {
+  int e = check_attn(d, "fbsa_fwd");
+  if (e) return e;
+  if (!q || !k || !v || !sel || !o) return fail(FBSA_EINVAL, "fbsa_fwd: null tensor pointer");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
+    return fail(FBSA_EINVAL, "fbsa_fwd: q/k/v/o must be 16-byte aligned");
+  if (!aligned(sel, 4) || (gate && !aligned(gate, 4)) || (lse && !aligned(lse, 4)))
+    return fail(FBSA_EINVAL, "fbsa_fwd: sel/gate/lse must be 4-byte aligned");
+  if (out_gate && !aligned(out_gate, esize(d->dtype)))
+    return fail(FBSA_EINVAL, "fbsa_fwd: out_gate misaligned");
+  FwdArgs a;
+  fill_fwd(d, a);
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse; a.sel = sel; a.gate = gate; a.og = out_gate;
+  return run_fwd(d, a, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// ---- entry points not implemented yet: report FBSA_EUNSUPPORTED ----
+extern "C" {
+int fbsa_pool(const fbsa_pool_desc *, const void *, void *, void *, void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_pool: not implemented");
+}
+size_t fbsa_select_workspace_bytes(const fbsa_select_desc *) { return 0; }
+int fbsa_select(const fbsa_select_desc *, const void *, const void *, const void *, int32_t *, float *, void *,
+                size_t, void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_select: not implemented");
+}
+int fbsa_bwd_prep(const fbsa_attn_desc *, const void *, const void *, float *, void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_prep: not implemented");
+}
+size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *) { return 0; }
+int fbsa_transpose_index(const fbsa_attn_desc *, const int32_t *, void *, size_t, void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_transpose_index: not implemented");
+}
+int fbsa_bwd_dq(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const void *,
+                const float *, const float *, const int32_t *, const float *, const void *, void *, float *, void *,
+                void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_dq: not implemented");
+}
+int fbsa_bwd_dkdv(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const float *,
+                  const float *, const int32_t *, const float *, const void *, const void *, size_t, void *, void *,
+                  void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_dkdv: not implemented");
+}
+int fbsa_bwd(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const void *,
+             const float *, const int32_t *, const float *, const void *, void *, void *, void *, float *, void *,
+             void *, size_t, void *) {
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: not implemented");
+}
+}

@@ -1,0 +1,136 @@
+// Shared device/host helpers for the gfx950 block-sparse attention kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fbsa.h"
+
+namespace fbsa {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---- host-side error reporting (thread-local message, status code) ----
+int fail(int code, const char *fmt, ...);
+int hip_check(hipError_t e, const char *what);
+
+// ---- element conversions ----
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// ---- LDS chunk swizzle -----------------------------------------------------
+// A tile row of cpr 16-byte chunks stores logical chunk c at position
+// c ^ swz(row). The patterns keep (a) the 16 rows x one chunk read by an MFMA
+// A/B-operand load and (b) the 8 rows x two adjacent chunks read by a
+// transposing LDS load on distinct banks (64 banks x 4 bytes).
+__host__ __device__ constexpr int swz(int row, int cpr) {
+  return cpr >= 16 ? (((row & 7) << 1) | ((row >> 3) & 1))
+       : cpr == 8  ? ((((row >> 1) & 3) << 1) | ((row >> 3) & 1))
+       : cpr == 4  ? ((((row >> 2) & 1) << 1) | ((row >> 3) & 1))
+       : 0;
+}
+
+// ---- gfx950 primitives ----------------------------------------------------
+// 16-byte global -> LDS copy: lane l's bytes land at lds_wave_base + 16*l.
+__device__ __forceinline__ void g2lds16(const void *gsrc, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
+                                   (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] at bits 3:0, vmcnt[5:4] at bits 15:14, expcnt/lgkmcnt left open).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Workgroup barrier for LDS-staged pipelines. Unlike __syncthreads() it does
+// not wait for outstanding vector-memory ops (which would drain the
+// direct-to-LDS prefetch ring); callers wait for their own DMA with
+// wait_vmcnt<N>() first. Pending LDS reads are drained (lgkmcnt(0)) and the
+// empty asm statements keep the compiler from moving memory ops across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16). Within each 16-lane group, lane i
+// supplies the address of 4 consecutive 16-bit elements C[i][0..3]; lane j
+// receives C[4e + j/4][j%4] for e = 0..3.
+// Issued as inline asm: the compiler's builtin form makes it wait for every
+// outstanding direct-to-LDS load first, which would drain the prefetch ring.
+// The result is NOT ready until lds_wait_all() and must pass through
+// lds_ready() before use.
+__device__ __forceinline__ s16x4 lds_read_tr16(const void *lds_addr) {
+  s16x4 r;
+  const unsigned a = (unsigned)(uintptr_t)lds_addr;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <typename V> __device__ __forceinline__ void lds_ready(V &x) { asm volatile("" : "+v"(x)); }
+
+__device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
+
+// MFMA 16x16x32 (bf16 / f16 inputs, fp32 accumulate). Operand lane layout:
+// lane l holds row/col (l % 16) and k = 8*(l/16) + e, e = 0..7 (any k
+// permutation works if A and B agree). Result: lane l holds rows 4*(l/16)+r,
+// column l % 16, r = 0..3.
+template <typename T> struct Mfma16;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+template <> struct Mfma16<bf16> {
+  __device__ static __forceinline__ f32x4 run(s16x8 a, s16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // k = 16 variant: lane l holds k = 4*(l/16) + e, e = 0..3
+  __device__ static __forceinline__ f32x4 run16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16> {
+  __device__ static __forceinline__ f32x4 run(s16x8 a, s16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ f32x4 run16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+
+// fp32 MFMA 16x16x4: lane l holds row/col l%16, k = l/16.
+__device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <typename T> __device__ __forceinline__ short bits16(T x) { return __builtin_bit_cast(short, x); }
+
+// Pack 8 fp32 into 8 16-bit values of type T.
+template <typename T> __device__ __forceinline__ s16x8 pack8(const float *x) {
+  s16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = bits16<T>((T)x[e]);
+  return r;
+}
+
+// XCD-aware work order: launch order bid is dispatched round-robin over the
+// 8 XCDs; returning w = (bid % 8) * (n / 8) + bid / 8 gives each XCD a
+// contiguous range of the work order (the tail beyond 8*(n/8) maps 1:1).
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
+  const int64_t per = n / 8;
+  if (bid >= per * 8) return bid;
+  return (bid % 8) * per + bid / 8;
+}
+
+}  // namespace fbsa

@@ -1,0 +1,26 @@
+// Kernel argument blocks and launch entry points shared by the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fbsa.h"
+
+namespace fbsa {
+
+struct FwdArgs {
+  const void *q, *k, *v;
+  void *o;
+  float *lse;
+  const int32_t *sel;
+  const float *gate;
+  const void *og;
+  int64_t B, Hq, Hkv, L, nblk, kk, hsel, l_valid;
+  int64_t sq[3], sk[3], sv[3], so[3], sog[3];
+  float scale2;  // softmax scale * log2(e)
+  int mask;
+  int grp;
+};
+
+int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
+
+}  // namespace fbsa

@@ -1,0 +1,168 @@
+/*
+ * fbsa.h -- C ABI of the MI355X (gfx950) block-pair selection + fused
+ * block-sparse attention library (libfbsa.so).
+ *
+ * Every entry point is stateless and re-entrant, takes raw device pointers,
+ * 64-bit sizes/strides in elements, and the HIP stream to launch on (passed as
+ * void*, a hipStream_t; NULL = the default stream). Nothing here allocates
+ * device memory: workspaces are sized by the *_workspace_bytes queries and
+ * provided by the caller. Arguments are validated on the host before any
+ * launch; a non-zero status is returned with a message in fbsa_last_error()
+ * (thread-local). Launches are asynchronous.
+ *
+ * Tensor layouts (element strides; the innermost dimension D is contiguous):
+ *   q, o, do, dq   (B, Hq, L, D)   strides {b, h, l}
+ *   k, v, dk, dv   (B, Hkv, L, D)  strides {b, h, l}
+ *   out_gate       (B, Hq, L, D)   strides {b, h, l} (e.g. Qwen's (B,L,Hq*D) view)
+ *   sel, gate      (B, Hsel, nblk, kk) contiguous, int32 / fp32; Hsel = 1
+ *                  (one selection shared by every head) or Hkv (per KV head)
+ *   lse, delta     (B, Hq, L) contiguous fp32
+ *
+ * The reference (apoc/fused-block-sparse-attention) is Python + Triton; the
+ * entry points below replace the device work behind its Python surfaces, as
+ * cited on each declaration.
+ */
+#ifndef FBSA_H
+#define FBSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of float tensors (q, k, v, o, do, dq, dk, dv, out_gate, pooled operands). */
+enum { FBSA_F32 = 0, FBSA_BF16 = 1, FBSA_F16 = 2 };
+
+/* Attention mask rules.
+ * NONE         every key of every slot (src/triton_kernel.py:20-74 with CAUSAL=False)
+ * SLOT_CAUSAL  slot 0: key row <= query row; slot s>0 valid iff sel < i
+ *              (src/triton_kernel.py:57-61; src/ssa_model.py:167-183)
+ * TOKEN_CAUSAL key pos <= query pos, key pos < l_valid, first occurrence of the
+ *              block index in the row (src/qwen_blocksparse.py:67-72) */
+enum { FBSA_MASK_NONE = 0, FBSA_MASK_SLOT_CAUSAL = 1, FBSA_MASK_TOKEN_CAUSAL = 2 };
+
+/* Status codes. */
+enum { FBSA_OK = 0, FBSA_EINVAL = 1, FBSA_EUNSUPPORTED = 2, FBSA_EHIP = 3, FBSA_EWORKSPACE = 4 };
+
+typedef struct fbsa_attn_desc {
+  int32_t dtype;   /* FBSA_F32 / FBSA_BF16 / FBSA_F16 */
+  int32_t mask;    /* FBSA_MASK_* */
+  int64_t B, Hq, Hkv;
+  int64_t L;       /* sequence length, a multiple of bs (nblk * bs) */
+  int64_t D;       /* head dim: 32, 64, 128 or 256 */
+  int64_t bs;      /* block size: 16, 32, 64 or 128 */
+  int64_t nblk, kk;
+  int64_t hsel;    /* 1 or Hkv */
+  int64_t l_valid; /* positions >= l_valid are padding keys (TOKEN_CAUSAL) */
+  float scale;     /* softmax scale applied to q.k before the gate bias */
+  int32_t flags;   /* reserved, 0 */
+  int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sog[3];
+} fbsa_attn_desc;
+
+const char *fbsa_last_error(void);
+int fbsa_version(void);
+
+/* Fused block-sparse forward. o = softmax(scale*q.k^T + gate) v over the
+ * selected key blocks (times sigmoid(out_gate) when out_gate != NULL);
+ * lse (nullable) = natural-log normaliser of the un-gated softmax.
+ * gate (nullable): fp32 additive bias per (b, hsel, i, slot).
+ * Replaces _bsattn_fwd / bsattn_forward (src/triton_kernel.py:20-74, 184-207)
+ * and the gather+SDPA of _gather_and_attend (src/ssa_model.py:57-90) and
+ * blocksparse_forward (src/qwen_blocksparse.py:57-84). */
+int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
+             const int32_t *sel, const float *gate, const void *out_gate,
+             void *o, float *lse, void *stream);
+
+/* ---- selection ------------------------------------------------------- */
+
+/* Pooling ops over each block of bs tokens (tokens >= l_valid read as 0).
+ * MEAN_TOK_THEN_GRP  mean over tokens (rounded), then over the grp heads
+ *                    (rounded): q.view(B,H,nblk,bs,D).mean(3).mean(1)
+ *                    (src/ssa_model.py:287-288)
+ * MEAN_GRP_THEN_TOK  mean over the grp heads (rounded), then tokens (rounded)
+ *                    (src/qwen_blocksparse.py:113)
+ * MAX / MIN          per-block max / min (src/ssa_model.py:117;
+ *                    src/qwen_blocksparse.py:115-116)
+ * MINMAX             min into out, max into out2 */
+enum { FBSA_POOL_MEAN_TOK_THEN_GRP = 0, FBSA_POOL_MEAN_GRP_THEN_TOK = 1,
+       FBSA_POOL_MAX = 2, FBSA_POOL_MIN = 3, FBSA_POOL_MINMAX = 4 };
+
+typedef struct fbsa_pool_desc {
+  int32_t dtype, op;
+  int64_t B, H, L, D, bs, nblk, grp, l_valid;
+  int64_t sx[3];   /* input strides {b, h, l}; output (B, H/grp, nblk, D) contiguous */
+} fbsa_pool_desc;
+
+int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, void *stream);
+
+/* Score functions of the nblk x nblk pooled contraction (never stored):
+ * DOT    rnd(a.b1)                                   (src/scale_sel.py:33-35)
+ * MAX2   max(rnd(a.b1), rnd(a.b2))                   (src/ssa_model.py:118-119)
+ * QUEST  rnd(rnd(relu(a).b1) + rnd(min(a,0).b2))     (src/qwen_blocksparse.py:117-120)
+ * rnd() rounds the exact value to fp32 and then to the operand dtype. */
+enum { FBSA_SCORE_DOT = 0, FBSA_SCORE_MAX2 = 1, FBSA_SCORE_QUEST = 2 };
+/* OWN_FIRST:   sel = [i, top-k content blocks by descending score], own block
+ *              excluded, future blocks excluded when causal, fills = i
+ *              (src/ssa_model.py:151-165)
+ * SORTED_SINK: _finish: top-k over j <= i (own included), non-finite picks
+ *              -> i, + own (+ sink block 0), sorted ascending
+ *              (src/qwen_blocksparse.py:87-99) */
+enum { FBSA_SEL_OWN_FIRST = 0, FBSA_SEL_SORTED_SINK = 1 };
+
+typedef struct fbsa_select_desc {
+  int32_t dtype, score, convention, causal, sink, flags;
+  int64_t B, H, nblk, D, topk, kk;  /* operands (B, H, nblk, D) contiguous */
+} fbsa_select_desc;
+
+/* Streaming score + top-k: writes sel (B,H,nblk,kk) int32 and, when sel_score
+ * != NULL, the score of each chosen slot as fp32 (for the log-sigmoid gate).
+ * Ties break towards the lower block index.
+ * Replaces the topk selection of src/ssa_model.py:151-165,
+ * src/bench_crossover.py:41-54 and SelectMax/_finish
+ * (src/qwen_blocksparse.py:87-121). */
+size_t fbsa_select_workspace_bytes(const fbsa_select_desc *d);
+int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2,
+                int32_t *sel, float *sel_score, void *workspace, size_t workspace_bytes,
+                void *stream);
+
+/* ---- backward -------------------------------------------------------- */
+
+/* delta[b,h,t] = sum_d do*o (o as written by fbsa_fwd, gated or not). */
+int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, float *delta,
+                  void *stream);
+
+/* Block-transposed index: for each (b, hsel, key block j) the (i, slot)
+ * pairs that attend to it, in ascending (i, slot) order (deterministic CSR).
+ * Uses the workspace; must precede fbsa_bwd_dkdv. */
+size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *d);
+int fbsa_transpose_index(const fbsa_attn_desc *d, const int32_t *sel, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/* dq (B,Hq,L,D contiguous) and, when dgate != NULL, the fp32 gate gradient
+ * (B,Hsel,nblk,kk); when out_gate != NULL also dout_gate (strides sog). */
+int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
+                const void *o, const void *dout, const float *lse, const float *delta,
+                const int32_t *sel, const float *gate, const void *out_gate,
+                void *dq, float *dgate, void *dout_gate, void *stream);
+
+/* dk, dv (B,Hkv,L,D contiguous), atomics-free over the transposed index. */
+int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
+                  const void *dout, const float *lse, const float *delta,
+                  const int32_t *sel, const float *gate, const void *out_gate,
+                  const void *workspace, size_t workspace_bytes,
+                  void *dk, void *dv, void *stream);
+
+/* All of the above in order. Replaces _bsattn_bwd / bsattn_backward
+ * (src/triton_kernel.py:77-181, 210-234). */
+int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
+             const void *o, const void *dout, const float *lse, const int32_t *sel,
+             const float *gate, const void *out_gate, void *dq, void *dk, void *dv,
+             float *dgate, void *dout_gate, void *workspace, size_t workspace_bytes,
+             void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FBSA_H */

@@ -1,0 +1,235 @@
+"""Selection oracle: pooling, pooled scores, conventions A and B (test infrastructure only).
+
+Restates, in numpy, the reference's block-pair selection:
+
+* ``pool_mean_tok_then_heads`` -- ``q.view(B,H,nblk,Bs,dh).mean(3).mean(1)``
+  (``src/ssa_model.py:287-288``): the mean-pooled q/k selector used by the
+  synthetic configurations (the contraction is ``src/scale_sel.py:33-35``).
+* ``pool_mean_grp_then_tok`` / ``pool_minmax`` -- ``SelectMax.select``
+  (``src/qwen_blocksparse.py:111-116``).
+* ``pool_tok`` -- ``BlockSparseSSA._scores`` pooling (``src/ssa_model.py:114-117``).
+* ``scores`` -- the nblk x nblk contraction: plain dot (``src/scale_sel.py:33``),
+  max of two dots (``src/ssa_model.py:118-119``), Quest q+/q- split
+  (``src/qwen_blocksparse.py:117-120``), each rounded where torch rounds.
+* ``select_conv_a`` -- own block first + top-k content blocks
+  (``src/ssa_model.py:151-165``; ``src/bench_crossover.py:41-54``).
+* ``select_conv_b`` -- ``_finish`` (``src/qwen_blocksparse.py:87-99``).
+
+Tie-break: candidates are ranked NaN first (torch.topk treats NaN as the
+largest value), then by descending score, then by ascending block index.
+torch.topk's order among exactly equal scores is implementation-defined; the
+lowest-index rule is this build's canonical choice and ``near_tie_rows``
+implements the parity procedure for comparing against any other order.
+"""
+import numpy as np
+
+from .numerics import round_to
+
+
+def _pad_tokens(x, bs, axis):
+    """Zero-pad the token axis to a multiple of bs (``_pad_blocks``,
+    ``src/qwen_blocksparse.py:20-26``; ``F.pad`` in ``src/ssa_model.py:124-126``)."""
+    n = x.shape[axis]
+    nblk = (n + bs - 1) // bs
+    pad = nblk * bs - n
+    if pad:
+        widths = [(0, 0)] * x.ndim
+        widths[axis] = (0, pad)
+        x = np.pad(x, widths)
+    return x, nblk
+
+
+def pool_mean_tok_then_heads(x, bs, dtype):
+    """(B,H,N,D) -> (B,nblk,D): mean over the block's tokens (rounded), then
+    over heads (rounded). ``src/ssa_model.py:287-288``."""
+    x = np.asarray(x, dtype=np.float64)
+    B, H, N, D = x.shape
+    x, nblk = _pad_tokens(x, bs, 2)
+    tok = round_to(x.reshape(B, H, nblk, bs, D).sum(axis=3) / bs, dtype)
+    return round_to(tok.sum(axis=1) / H, dtype)
+
+
+def pool_mean_grp_then_tok(q, hkv, bs, dtype):
+    """(B,Hq,N,D) -> (B,Hkv,nblk,D): mean over the GQA group (rounded), then
+    over the block's tokens (rounded). ``src/qwen_blocksparse.py:113``."""
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, N, D = q.shape
+    grp = Hq // hkv
+    q, nblk = _pad_tokens(q, bs, 2)
+    g = round_to(q.reshape(B, hkv, grp, nblk, bs, D).sum(axis=2) / grp, dtype)
+    return round_to(g.sum(axis=3) / bs, dtype)
+
+
+def pool_minmax(k, bs):
+    """(B,H,N,D) -> kmin, kmax (B,H,nblk,D), exact. Padding rows are zeros and
+    take part, as in ``src/qwen_blocksparse.py:112-116``."""
+    k = np.asarray(k, dtype=np.float64)
+    B, H, N, D = k.shape
+    k, nblk = _pad_tokens(k, bs, 2)
+    kb = k.reshape(B, H, nblk, bs, D)
+    return kb.min(axis=3), kb.max(axis=3)
+
+
+def pool_tok(x, bs, dtype, op):
+    """(B,N,S) -> (B,nblk,S): per-block token mean (rounded) or max (exact).
+    ``src/ssa_model.py:114-117`` (N is already a multiple of bs there)."""
+    x = np.asarray(x, dtype=np.float64)
+    B, N, S = x.shape
+    x, nblk = _pad_tokens(x, bs, 1)
+    xb = x.reshape(B, nblk, bs, S)
+    if op == "mean":
+        return round_to(xb.sum(axis=2) / bs, dtype)
+    if op == "max":
+        return xb.max(axis=2)
+    if op == "min":
+        return xb.min(axis=2)
+    raise ValueError(op)
+
+
+def _seq_dot(a, b, rows=None):
+    """Exact-order dot products: s = sum_d a[..,i,d]*b[..,j,d] accumulated
+    sequentially over d in float64 (the GPU kernel uses the same order with
+    fp64 FMA, and the bf16/fp32 products are exact in fp64)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    if rows is not None:
+        a = a[..., rows, :]
+    out = np.zeros(a.shape[:-1] + (b.shape[-2],), dtype=np.float64)
+    for d in range(a.shape[-1]):
+        out += a[..., :, None, d] * b[..., None, :, d]
+    return out
+
+
+def scores(a, b1, dtype, combine="dot", b2=None, rows=None):
+    """Pooled block-pair scores (..., nblk_q, nblk_k), rounded like torch.
+
+    combine='dot'   : rnd(a . b1)                                (src/scale_sel.py:33)
+    combine='max2'  : max(rnd(a . b1), rnd(a . b2))              (src/ssa_model.py:118-119)
+    combine='quest' : rnd(rnd(relu(a) . b1) + rnd(min(a,0) . b2)) with b1=kmax,
+                      b2=kmin                                    (src/qwen_blocksparse.py:117-120)
+    ``rows`` restricts the query-block rows computed (for large nblk).
+    """
+    if combine == "dot":
+        return round_to(_seq_dot(a, b1, rows), dtype)
+    if combine == "max2":
+        return np.maximum(round_to(_seq_dot(a, b1, rows), dtype),
+                          round_to(_seq_dot(a, b2, rows), dtype))
+    if combine == "quest":
+        a = np.asarray(a, dtype=np.float64)
+        s1 = round_to(_seq_dot(np.maximum(a, 0.0), b1, rows), dtype)
+        s2 = round_to(_seq_dot(np.minimum(a, 0.0), b2, rows), dtype)
+        return round_to(s1 + s2, dtype)
+    raise ValueError(combine)
+
+
+def _rank(score, valid):
+    """Per-row candidate order: valid NaN first, then valid by descending
+    score, then invalid; ties by ascending index (stable)."""
+    score = np.asarray(score, dtype=np.float64)
+    nan = np.isnan(score)
+    cls = np.where(valid, np.where(nan, 0, 1), 2)
+    neg = np.where(nan, 0.0, -score)
+    idx = np.broadcast_to(np.arange(score.shape[-1]), score.shape)
+    return np.lexsort((idx, neg, cls), axis=-1)
+
+
+def select_conv_a(raw, topk, causal, rows=None):
+    """Convention A (``src/ssa_model.py:151-165``).
+
+    raw: (B, nblk_rows, nblk) scores for query-block rows ``rows`` (all rows by
+    default). Returns sel (B, R, kk) int64 with kk = 1 + min(topk, nblk-1):
+    slot 0 = own block i; slots 1.. = content blocks by descending score with
+    the diagonal (and, if causal, every j > i) excluded. Rows with fewer valid
+    candidates than the budget (causal, i < kk-1) are filled with i; the
+    slot-causal mask rule (slot s>0 valid iff sel < i) masks those fills, as it
+    masks torch.topk's -inf picks in the reference.
+    """
+    raw = np.asarray(raw, dtype=np.float64)
+    B, R, nblk = raw.shape
+    rows = np.arange(R) if rows is None else np.asarray(rows)
+    j = np.arange(nblk)
+    valid = j[None, :] != rows[:, None]
+    if causal:
+        valid &= j[None, :] < rows[:, None]
+    valid = np.broadcast_to(valid, raw.shape)
+    kk_c = min(topk, nblk - 1)
+    own = np.broadcast_to(rows[None, :, None], (B, R, 1)).astype(np.int64)
+    if kk_c <= 0:
+        return own.copy()
+    order = _rank(raw, valid)[..., :kk_c]
+    ok = np.take_along_axis(valid, order, axis=-1)
+    picks = np.where(ok, order, own)
+    return np.concatenate([own, picks], axis=-1).astype(np.int64)
+
+
+def select_conv_b(score, topk, sink, rows=None):
+    """Convention B, ``_finish`` (``src/qwen_blocksparse.py:87-99``).
+
+    score: (B, H, R, nblk). Future blocks j > i are masked to -inf (own NOT
+    excluded); the top min(topk, nblk) picks whose score is not finite become
+    the own block; own (and block 0 when ``sink``) are appended and each row is
+    sorted ascending. Duplicates are kept (the attention rule dedups them).
+    """
+    score = np.asarray(score, dtype=np.float64)
+    B, H, R, nblk = score.shape
+    rows = np.arange(R) if rows is None else np.asarray(rows)
+    j = np.arange(nblk)
+    fut = j[None, :] > rows[:, None]
+    masked = np.where(fut, -np.inf, score)
+    kk_t = min(topk, nblk)
+    order = _rank(masked, np.ones_like(masked, dtype=bool))[..., :kk_t]
+    vals = np.take_along_axis(masked, order, axis=-1)
+    own = np.broadcast_to(rows[None, None, :, None], (B, H, R, 1)).astype(np.int64)
+    picks = np.where(np.isfinite(vals), order, own)
+    parts = [picks, own]
+    if sink:
+        parts.append(np.zeros((B, H, R, 1), dtype=np.int64))
+    return np.sort(np.concatenate(parts, axis=-1), axis=-1).astype(np.int64)
+
+
+def gate_from_scores(raw, sel):
+    """gate[b,i,s] = logsigmoid(raw[b,i,sel[b,i,s]]) (``src/ssa_model.py:189-191``),
+    float64 (the caller rounds to the score dtype if it mirrors torch)."""
+    g = np.take_along_axis(np.asarray(raw, dtype=np.float64), np.asarray(sel), axis=-1)
+    return -np.logaddexp(0.0, -g)
+
+
+def select_mean_pooled(q, k, bs, topk, causal, dtype):
+    """Configs 1/2/3/5 selector: mean-pooled q.k scores + convention A.
+    Returns (sel (B,nblk,kk) int64, raw (B,nblk,nblk))."""
+    qp = pool_mean_tok_then_heads(q, bs, dtype)
+    kp = pool_mean_tok_then_heads(k, bs, dtype)
+    raw = scores(qp, kp, dtype, "dot")
+    return select_conv_a(raw, topk, causal), raw
+
+
+def select_quest(q, k, bs, topk, sink, dtype):
+    """``SelectMax.select`` (``src/qwen_blocksparse.py:107-121``).
+    Returns (idx (B,Hkv,nblk,kk) int64, score (B,Hkv,nblk,nblk))."""
+    hkv = k.shape[1]
+    qpool = pool_mean_grp_then_tok(q, hkv, bs, dtype)
+    kmin, kmax = pool_minmax(k, bs)
+    sc = scores(qpool, kmax, dtype, "quest", b2=kmin)
+    return select_conv_b(sc, topk, sink), sc
+
+
+def near_tie_rows(score, sel_valid_sets, k_eff, valid_mask, rel=1e-6):
+    """Parity procedure for selected-set comparison (near-tie census).
+
+    score: (..., R, nblk) oracle scores; valid_mask: candidate validity of the
+    same shape; sel_valid_sets: (..., R, k_eff) chosen candidate indices (the
+    valid content picks). A row is a near-tie row if some valid candidate
+    outside the chosen set has |s - s_k| < rel * max(1, |s_k|), where s_k is
+    the k-th best chosen score. Returns a bool array (..., R).
+    """
+    score = np.asarray(score, dtype=np.float64)
+    chosen = np.zeros(score.shape, dtype=bool)
+    np.put_along_axis(chosen, np.asarray(sel_valid_sets), True, axis=-1)
+    chosen &= valid_mask
+    s_chosen = np.where(chosen, score, np.inf)
+    s_k = s_chosen.min(axis=-1, keepdims=True)
+    others = valid_mask & ~chosen & np.isfinite(score)
+    tol = rel * np.maximum(1.0, np.abs(s_k))
+    close = others & (np.abs(score - s_k) < tol)
+    has_k = np.isfinite(s_k[..., 0])
+    return close.any(axis=-1) & has_k
