@@ -21,6 +21,11 @@ namespace fbsa {
 
 enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2 };
 
+// LDS bytes per workgroup for the K/V prefetch ring (sets the ring depth).
+#ifndef FBSA_FWD_LDS_BUDGET
+#define FBSA_FWD_LDS_BUDGET 32768
+#endif
+
 template <typename T, int BS, int D> struct FwdCfg {
   static constexpr int ES = sizeof(T);
   static constexpr int NW = BS / 16;
@@ -31,7 +36,7 @@ template <typename T, int BS, int D> struct FwdCfg {
   static constexpr int TILE_BYTES = KC * D * ES;
   static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
   static constexpr int LPT = STAGE_BYTES / (NT * 16);
-  static constexpr int NS0 = 98304 / STAGE_BYTES;
+  static constexpr int NS0 = FBSA_FWD_LDS_BUDGET / STAGE_BYTES;
   static constexpr int NSTAGE = NS0 < 1 ? 1 : (NS0 > 4 ? 4 : NS0);
   static_assert(LPT * NT * 16 == STAGE_BYTES, "stage must split evenly over threads");
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
@@ -182,42 +187,50 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
       }
     }
 
-    // scale + gate + mask (log2 domain)
-    float sv[C::KC / 16][4];
+    // mask: key row u (within block j) is valid iff u <= lim (uniform branch
+    // skips the compares for unmasked chunks, the common case)
+    if (kind != KIND_FULL) {
+      const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
+                                              : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
+                                                                                            : a.l_valid - j * BS - 1);
+      const int lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;  // compare against 16m + r
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * m + r > lim) sacc[m][r] = -INFINITY;
+    }
+    // online softmax in the log2 domain; scale and gate are folded into one
+    // FMA per score: p = exp2(s * scale2 + (gate2 - m))
     float mloc = -INFINITY;
 #pragma unroll
-    for (int m = 0; m < C::KC / 16; ++m) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int u = ch * C::KC + 16 * m + 4 * g + r;  // key row in block j
-        bool ok = true;
-        if (kind == KIND_DIAG) ok = u <= tq;
-        else if (kind == KIND_ABS) ok = (j * BS + u <= i * BS + tq) && (j * BS + u < a.l_valid);
-        const float x = ok ? sacc[m][r] * a.scale2 + gt : -INFINITY;
-        sv[m][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    }
+    for (int m = 0; m < C::KC / 16; ++m)
+      mloc = fmaxf(mloc, fmaxf(fmaxf(sacc[m][0], sacc[m][1]), fmaxf(sacc[m][2], sacc[m][3])));
     mloc = fmaxf(mloc, shfl_xor_f(mloc, 16));
     mloc = fmaxf(mloc, shfl_xor_f(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
+    const float mchunk = mloc * a.scale2 + gt;  // -inf when every key is masked
+    const float m_new = fmaxf(m_run, mchunk);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    const float off = gt - m_use;
+    float sv[C::KC / 16][4];
     float psum = 0.f;
 #pragma unroll
     for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(sv[m][r] - m_use);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off));
         sv[m][r] = e;
         psum += e;
       }
-    l_run = l_run * alpha + psum;
+    l_run = __builtin_fmaf(l_run, alpha, psum);
     m_run = m_new;
+    if (__ballot(alpha != 1.f)) {  // rescale only when some row max moved
 #pragma unroll
-    for (int mt = 0; mt < D / 16; ++mt)
+      for (int mt = 0; mt < D / 16; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) oacc[mt][r] *= alpha;
+        for (int r = 0; r < 4; ++r) oacc[mt][r] *= alpha;
+    }
 
     // O^T += V^T P^T
     if constexpr (F32) {
