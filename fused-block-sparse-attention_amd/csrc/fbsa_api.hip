@@ -96,18 +96,55 @@ int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
   return run_fwd(d, a, (hipStream_t)stream);
 }
 
+int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, void *stream) {
+  if (!d) return fail(FBSA_EINVAL, "fbsa_pool: null descriptor");
+  if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_pool: bad dtype %d", d->dtype);
+  if (d->op < FBSA_POOL_MEAN_TOK_THEN_GRP || d->op > FBSA_POOL_MINMAX) return fail(FBSA_EINVAL, "fbsa_pool: bad op %d", d->op);
+  if (d->B < 1 || d->H < 1 || d->L < 1 || d->D < 8 || d->bs < 1 || d->nblk < 1 || d->grp < 1)
+    return fail(FBSA_EINVAL, "fbsa_pool: sizes must be positive (D >= 8)");
+  if (d->D % 8 || d->D > 2048) return fail(FBSA_EUNSUPPORTED, "fbsa_pool: D=%lld must be a multiple of 8 and <= 2048", (long long)d->D);
+  if (d->H % d->grp) return fail(FBSA_EINVAL, "fbsa_pool: H=%lld not a multiple of grp=%lld", (long long)d->H, (long long)d->grp);
+  if ((d->op >= FBSA_POOL_MAX) && d->grp != 1) return fail(FBSA_EINVAL, "fbsa_pool: min/max pooling needs grp == 1");
+  if (d->nblk != (d->L + d->bs - 1) / d->bs) return fail(FBSA_EINVAL, "fbsa_pool: nblk must be ceil(L/bs)");
+  if (d->l_valid < 1 || d->l_valid > d->L) return fail(FBSA_EINVAL, "fbsa_pool: l_valid outside [1, L]");
+  if (!x || !out || (d->op == FBSA_POOL_MINMAX && !out2)) return fail(FBSA_EINVAL, "fbsa_pool: null pointer");
+  const int64_t es = esize(d->dtype);
+  if (!aligned(x, 16) || !aligned(out, es) || (out2 && !aligned(out2, es))) return fail(FBSA_EINVAL, "fbsa_pool: misaligned pointer");
+  for (int k = 0; k < 3; ++k)
+    if (d->sx[k] < 0 || (d->sx[k] * es) % 16) return fail(FBSA_EINVAL, "fbsa_pool: stride[%d] must be a non-negative multiple of 16 bytes", k);
+  if (d->B * (d->H / d->grp) * d->nblk > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_pool: grid too large");
+  return run_pool(d, x, out, out2, (hipStream_t)stream);
+}
+
+size_t fbsa_select_workspace_bytes(const fbsa_select_desc *) { return 0; }
+
+int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
+                float *sel_score, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace; (void)workspace_bytes;
+  if (!d) return fail(FBSA_EINVAL, "fbsa_select: null descriptor");
+  if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_select: bad dtype %d", d->dtype);
+  if (d->score < FBSA_SCORE_DOT || d->score > FBSA_SCORE_QUEST) return fail(FBSA_EINVAL, "fbsa_select: bad score %d", d->score);
+  if (d->convention != FBSA_SEL_OWN_FIRST && d->convention != FBSA_SEL_SORTED_SINK)
+    return fail(FBSA_EINVAL, "fbsa_select: bad convention %d", d->convention);
+  if (d->B < 1 || d->H < 1 || d->nblk < 1 || d->topk < 0) return fail(FBSA_EINVAL, "fbsa_select: bad sizes");
+  int64_t K, kk;
+  if (d->convention == FBSA_SEL_OWN_FIRST) { K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1; kk = 1 + K; }
+  else { K = d->topk < d->nblk ? d->topk : d->nblk; kk = K + 1 + (d->sink ? 1 : 0); }
+  if (d->kk != kk) return fail(FBSA_EINVAL, "fbsa_select: kk=%lld but the convention gives %lld", (long long)d->kk, (long long)kk);
+  if (K > 62) return fail(FBSA_EUNSUPPORTED, "fbsa_select: top-k budget %lld > 62 is not supported", (long long)K);
+  if (!a || !b1 || !sel || (d->score != FBSA_SCORE_DOT && !b2)) return fail(FBSA_EINVAL, "fbsa_select: null pointer");
+  const int64_t es = esize(d->dtype);
+  if (!aligned(a, es) || !aligned(b1, 16) || (b2 && !aligned(b2, 16)) || !aligned(sel, 4) || (sel_score && !aligned(sel_score, 4)))
+    return fail(FBSA_EINVAL, "fbsa_select: misaligned pointer");
+  const int64_t ntile = (d->nblk + 7) / 8;
+  if (ntile * d->B * d->H > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select: grid too large");
+  return run_select(d, a, b1, b2, sel, sel_score, (hipStream_t)stream);
+}
+
 }  // extern "C"
 
 // ---- entry points not implemented yet: report FBSA_EUNSUPPORTED ----
 extern "C" {
-int fbsa_pool(const fbsa_pool_desc *, const void *, void *, void *, void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_pool: not implemented");
-}
-size_t fbsa_select_workspace_bytes(const fbsa_select_desc *) { return 0; }
-int fbsa_select(const fbsa_select_desc *, const void *, const void *, const void *, int32_t *, float *, void *,
-                size_t, void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_select: not implemented");
-}
 int fbsa_bwd_prep(const fbsa_attn_desc *, const void *, const void *, float *, void *) {
   return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_prep: not implemented");
 }

@@ -22,5 +22,8 @@ struct FwdArgs {
 };
 
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
+int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
+int run_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
+               float *sel_score, hipStream_t s);
 
 }  // namespace fbsa

@@ -1,0 +1,114 @@
+"""Block pooling and streaming block-pair selection over the C ABI (gfx950).
+
+The pooled-score matrix (nblk x nblk) is never materialised: ``select`` streams
+the candidates through a per-row top-k held in registers. Scores are computed
+exactly (float64) and rounded to the operand dtype where torch rounds, so the
+chosen blocks match the oracle bit for bit; ties break towards the lower block
+index.
+"""
+import torch
+
+from . import _lib
+from .ops import _dtype_code, _ptr, _require_cuda, _stream
+
+POOL_OPS = {"mean_tok_then_grp": _lib.POOL_MEAN_TOK_THEN_GRP,
+            "mean_grp_then_tok": _lib.POOL_MEAN_GRP_THEN_TOK,
+            "max": _lib.POOL_MAX, "min": _lib.POOL_MIN, "minmax": _lib.POOL_MINMAX}
+SCORES = {"dot": _lib.SCORE_DOT, "max2": _lib.SCORE_MAX2, "quest": _lib.SCORE_QUEST}
+
+
+def pool(x, bs, op, grp=1, l_valid=None):
+    """Pool x (B,H,L,D) over blocks of bs tokens (and groups of grp heads).
+
+    op: 'mean_tok_then_grp' (src/ssa_model.py:287-288 with grp=H),
+    'mean_grp_then_tok' (src/qwen_blocksparse.py:113), 'max', 'min' or
+    'minmax' (src/qwen_blocksparse.py:115-116; returns (min, max)).
+    Tokens at positions >= l_valid (default L) count as zeros, like the
+    reference's zero padding. Returns (B, H//grp, ceil(L/bs), D) in x's dtype.
+    """
+    _require_cuda(x)
+    if x.dim() != 4:
+        raise ValueError("fbsa.pool: x must be (B, H, L, D)")
+    B, H, L, D = x.shape
+    if x.stride(-1) != 1 or any((s * x.element_size()) % 16 for s in x.stride()[:-1]) or x.data_ptr() % 16:
+        x = x.contiguous()
+    nblk = (L + bs - 1) // bs
+    d = _lib.PoolDesc()
+    d.dtype = _dtype_code(x)
+    d.op = POOL_OPS[op]
+    d.B, d.H, d.L, d.D, d.bs, d.nblk, d.grp = B, H, L, D, bs, nblk, grp
+    d.l_valid = L if l_valid is None else int(l_valid)
+    d.sx[:] = (x.stride(0), x.stride(1), x.stride(2))
+    out = torch.empty(B, H // grp if H % grp == 0 else 1, nblk, D, dtype=x.dtype, device=x.device)
+    out2 = torch.empty_like(out) if op == "minmax" else None
+    _lib.check(_lib.load().fbsa_pool(d, _ptr(x), _ptr(out), _ptr(out2), _stream()), "fbsa_pool")
+    return (out, out2) if op == "minmax" else out
+
+
+def budget(convention, topk, nblk, sink=False):
+    """Slots per query block: A: 1 + min(topk, nblk-1); B: min(topk, nblk) + 1 + sink."""
+    if convention == "own_first":
+        return 1 + min(topk, nblk - 1)
+    return min(topk, nblk) + 1 + (1 if sink else 0)
+
+
+def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=True, sink=False,
+           need_scores=False):
+    """Top-k key blocks per query block from pooled operands (B,H,nblk,D).
+
+    convention 'own_first' (A, src/ssa_model.py:151-165): [i, top-k content
+    blocks by descending score]; 'sorted_sink' (B, ``_finish``,
+    src/qwen_blocksparse.py:87-99): top-k over j <= i, + own (+ sink 0), sorted.
+    Returns sel int32 (B,H,nblk,kk) (and fp32 scores of the chosen slots).
+    """
+    _require_cuda(a, b1, b2)
+    if a.dim() != 4 or a.shape != b1.shape or (b2 is not None and b2.shape != a.shape):
+        raise ValueError("fbsa.select: operands must be (B, H, nblk, D) of equal shape")
+    if a.dtype != b1.dtype or (b2 is not None and b2.dtype != a.dtype):
+        raise ValueError("fbsa.select: operands must share a dtype")
+    B, H, nblk, D = a.shape
+    a, b1 = a.contiguous(), b1.contiguous()
+    b2 = b2.contiguous() if b2 is not None else None
+    conv = {"own_first": _lib.SEL_OWN_FIRST, "sorted_sink": _lib.SEL_SORTED_SINK}[convention]
+    kk = budget(convention, topk, nblk, sink)
+    d = _lib.SelectDesc()
+    d.dtype = _dtype_code(a)
+    d.score = SCORES[score]
+    d.convention = conv
+    d.causal = 1 if causal else 0
+    d.sink = 1 if sink else 0
+    d.flags = 0
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = B, H, nblk, D, topk, kk
+    sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
+    sc = torch.empty(B, H, nblk, kk, dtype=torch.float32, device=a.device) if need_scores else None
+    lib = _lib.load()
+    _lib.check(lib.fbsa_select(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(sel), _ptr(sc), None, 0, _stream()),
+               "fbsa_select")
+    return (sel, sc) if need_scores else sel
+
+
+def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False):
+    """Synthetic-config selector: mean-pooled q.k block scores, convention A.
+
+    qpool = q.view(B,H,nblk,bs,D).mean(3).mean(1) (src/ssa_model.py:287-288),
+    raw = qpool kpool^T (src/scale_sel.py:33), then own block + top-k content
+    blocks (src/ssa_model.py:151-165). Returns sel (B, nblk, kk) int32.
+    """
+    H = q.shape[1]
+    qp = pool(q, bs, "mean_tok_then_grp", grp=H)
+    kp = pool(k, bs, "mean_tok_then_grp", grp=k.shape[1])
+    out = select(qp, kp, score="dot", convention="own_first", topk=topk, causal=causal, need_scores=need_scores)
+    if need_scores:
+        return out[0][:, 0], out[1][:, 0]
+    return out[:, 0]
+
+
+def select_quest(q, k, bs, topk, sink=True, l_valid=None):
+    """SelectMax (src/qwen_blocksparse.py:107-121): Quest upper-bound scores
+    relu(qpool).kmax + min(qpool,0).kmin per KV head, then ``_finish``.
+    Returns idx (B, Hkv, nblk, kk) int32."""
+    Hkv = k.shape[1]
+    grp = q.shape[1] // Hkv
+    qpool = pool(q, bs, "mean_grp_then_tok", grp=grp, l_valid=l_valid)
+    kmin, kmax = pool(k, bs, "minmax", l_valid=l_valid)
+    return select(qpool, kmax, kmin, score="quest", convention="sorted_sink", topk=topk, sink=sink)

@@ -1,0 +1,156 @@
+"""GPU parity: pooling and streaming selection (libfbsa.so) vs the CPU oracle.
+
+Block indices must match bit for bit (ties break to the lower index in both);
+pooled values must match exactly (same rounding points)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import select as osel
+from _util import randn, np64
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(*a):
+    print("[select]", *a, flush=True)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_pool_mean_tok_then_heads_exact(dtype):
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(0)
+    B, H, N, D, bs = 2, 4, 1000, 64, 64          # N % bs != 0: zero-padded tail block
+    x = randn(g, (B, H, N, D), dtype)
+    _say("pool mean_tok_then_grp", dtype)
+    got = np64(selection.pool(x.to(DEV), bs, "mean_tok_then_grp", grp=H))
+    ref = osel.pool_mean_tok_then_heads(np64(x), bs, dtype)[:, None]
+    assert np.array_equal(got, ref), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_pool_quest_exact(dtype):
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(1)
+    B, Hq, Hkv, N, D, bs = 1, 8, 2, 700, 128, 128
+    q = randn(g, (B, Hq, N, D), dtype)
+    k = randn(g, (B, Hkv, N, D), dtype)
+    _say("pool quest", dtype)
+    qp = np64(selection.pool(q.to(DEV), bs, "mean_grp_then_tok", grp=Hq // Hkv))
+    kmin, kmax = selection.pool(k.to(DEV), bs, "minmax")
+    assert np.array_equal(qp, osel.pool_mean_grp_then_tok(np64(q), Hkv, bs, dtype))
+    rmin, rmax = osel.pool_minmax(np64(k), bs)
+    assert np.array_equal(np64(kmin), rmin) and np.array_equal(np64(kmax), rmax)
+
+
+def _check_sel(got, ref, what):
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{what}: {len(bad)} mismatching slots, first at {bad[:3].tolist()}: " \
+                          f"got {got[tuple(bad[0][:-1])]} ref {ref[tuple(bad[0][:-1])]}"
+
+
+@pytest.mark.parametrize("dtype,B,H,N,bs,topk,causal", [
+    ("f32", 1, 4, 4096, 64, 8, True),      # config 1
+    ("bf16", 32, 8, 1024, 32, 4, True),    # config 2
+    ("bf16", 1, 2, 8192, 16, 16, True),    # many blocks, small block
+    ("bf16", 2, 2, 2048, 64, 5, False),    # non-causal
+    ("f16", 1, 2, 2048, 32, 12, True),
+])
+def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal):
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(2)
+    D = 64
+    q, k = (randn(g, (B, H, N, D), dtype) for _ in range(2))
+    _say("mean-pooled", dtype, B, H, N, bs, topk, causal)
+    sel, sc = selection.select_mean_pooled(q.to(DEV), k.to(DEV), bs, topk, causal, need_scores=True)
+    ref, raw = osel.select_mean_pooled(np64(q), np64(k), bs, topk, causal, dtype)
+    _check_sel(sel.cpu().numpy(), ref, "sel")
+    ref_sc = np.take_along_axis(raw, ref, axis=-1)
+    assert np.array_equal(sc.cpu().numpy().astype(np.float64), ref_sc)
+
+
+def test_select_config3_full_size_sampled_rows():
+    # config 3: B1 H8 N262144 D64 bs64 top-16; q,k ~ N(0,1)/8 in bf16. The oracle
+    # pools the full tensors and scores a sample of rows (each row i depends
+    # only on qpool[i] and kpool[0..i]).
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(0)
+    B, H, N, D, bs, topk = 1, 8, 262144, 64, 64, 16
+    q = randn(g, (B, H, N, D), "bf16", scale=0.125)
+    k = randn(g, (B, H, N, D), "bf16", scale=0.125)
+    _say("config 3 selection")
+    sel = selection.select_mean_pooled(q.to(DEV), k.to(DEV), bs, topk, True).cpu().numpy()
+    qp = osel.pool_mean_tok_then_heads(np64(q), bs, "bf16")
+    kp = osel.pool_mean_tok_then_heads(np64(k), bs, "bf16")
+    rows = np.unique(np.concatenate([np.arange(0, 40), np.arange(4096 - 40, 4096),
+                                     np.random.default_rng(0).integers(0, 4096, 200)]))
+    raw = osel.scores(qp, kp, "bf16", "dot", rows=rows)
+    ref = osel.select_conv_a(raw, topk, True, rows=rows)
+    _check_sel(sel[:, rows], ref, "sel (sampled rows)")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_select_quest_config4_shape(dtype):
+    # config 4 selector: Hq16 Hkv2 D256 bs128 nblk512 top-32 + own + sink
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, N, D, bs, topk = 1, 16, 2, 65536, 256, 128, 32
+    q = randn(g, (B, Hq, N, D), dtype)
+    k = randn(g, (B, Hkv, N, D), dtype)
+    _say("quest config 4", dtype)
+    idx = selection.select_quest(q.to(DEV), k.to(DEV), bs, topk, sink=True).cpu().numpy()
+    ref, _ = osel.select_quest(np64(q), np64(k), bs, topk, True, dtype)
+    _check_sel(idx, ref, "idx")
+
+
+def test_select_max2_module_scores():
+    # BlockSparseSSA._scores: max(sq . sk_mean, sq . sk_max) (src/ssa_model.py:113-119)
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(4)
+    B, L, S, bs, topk = 2, 2048, 32, 64, 8
+    sq = randn(g, (B, 1, L, S), "bf16")
+    sk = randn(g, (B, 1, L, S), "bf16")
+    _say("max2")
+    a = selection.pool(sq.to(DEV), bs, "mean_tok_then_grp")
+    km = selection.pool(sk.to(DEV), bs, "mean_tok_then_grp")
+    kx = selection.pool(sk.to(DEV), bs, "max")
+    sel, sc = selection.select(a, km, kx, score="max2", topk=topk, causal=True, need_scores=True)
+    ra = osel.pool_tok(np64(sq)[:, 0], bs, "bf16", "mean")
+    rkm = osel.pool_tok(np64(sk)[:, 0], bs, "bf16", "mean")
+    rkx = osel.pool_tok(np64(sk)[:, 0], bs, "bf16", "max")
+    raw = osel.scores(ra, rkm, "bf16", "max2", b2=rkx)
+    ref = osel.select_conv_a(raw, topk, True)
+    _check_sel(sel.cpu().numpy()[:, 0], ref, "sel")
+    assert np.array_equal(sc.cpu().numpy()[:, 0].astype(np.float64), np.take_along_axis(raw, ref, -1))
+
+
+@pytest.mark.parametrize("nblk,topk,conv", [(1, 4, "own_first"), (3, 8, "own_first"), (5, 0, "own_first"),
+                                            (1, 4, "sorted_sink"), (4, 9, "sorted_sink"), (70, 62, "own_first")])
+def test_select_edge_budgets(nblk, topk, conv):
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(5)
+    a = randn(g, (1, 2, nblk, 32), "bf16")
+    b = randn(g, (1, 2, nblk, 32), "bf16")
+    _say("edge", nblk, topk, conv)
+    sel = selection.select(a.to(DEV), b.to(DEV), topk=topk, convention=conv, sink=conv == "sorted_sink").cpu().numpy()
+    raw = osel.scores(np64(a), np64(b), "bf16", "dot")
+    if conv == "own_first":
+        ref = np.stack([osel.select_conv_a(raw[:, h], topk, True) for h in range(2)], 1)
+    else:
+        ref = osel.select_conv_b(raw, topk, True)
+    _check_sel(sel, ref, "sel")
+
+
+def test_select_ties_break_to_lower_index():
+    # all-equal scores: every candidate ties; lowest indices must win
+    from fbsa_amd import selection
+    nblk, topk = 200, 7
+    a = torch.ones(1, 1, nblk, 16, dtype=torch.bfloat16)
+    sel = selection.select(a.to(DEV), a.to(DEV), topk=topk, causal=True).cpu().numpy()[0, 0]
+    for i in range(nblk):
+        want = [i] + [j for j in range(min(i, topk))] + [i] * max(0, topk - i)
+        assert sel[i].tolist() == want, (i, sel[i])
