@@ -1,0 +1,194 @@
+"""Benchmark: block-pair selection + fused block-sparse forward on one MI355X.
+
+Workload (the north-star shape): bf16, B=1, H=8,
+D=64, N=262144, block 64 (nblk=4096), causal, top-16 content blocks by
+mean-pooled q.k scores (kk=17), q,k,v ~ N(0,1)/sqrt(D). One step = pool q,
+pool k, streaming top-k selection, fused forward (plus the backward when
+--bwd is given), all on device-resident inputs.
+
+Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step;
+``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
+FLOP per launch, the reference's own formula, src/bench_crossover.py:105)
+timed with HIP events on the launch stream; ``cpu_baseline`` times the CPU
+oracle (numpy restatement of the reference gather path) on a bounded sample
+of query blocks and scales it to the whole workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "fused-block-sparse-attention_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--N", type=int, default=262144)
+    p.add_argument("--H", type=int, default=8)
+    p.add_argument("--D", type=int, default=64)
+    p.add_argument("--bs", type=int, default=64)
+    p.add_argument("--topk", type=int, default=16)
+    p.add_argument("--bwd", action="store_true", help="also time the backward (separate fields)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--cpu-rows", type=int, default=128, help="query blocks in the CPU sample")
+    return p.parse_args()
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    copy-kernel calibrated) and recorded in profiles/traffic.json; None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[workload][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(q, k, v, bs, topk, rows_wanted):
+    """Time the CPU oracle on a bounded sample: full pooling, then scores +
+    convention-A selection + gather attention for `rows_wanted` query blocks
+    spread over the sequence; scale to the whole workload."""
+    import numpy as np
+    from oracle import attn as oattn, select as osel
+
+    f64 = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
+    qh, kh, vh = f64(q), f64(k), f64(v)
+    B, H, N, D = qh.shape
+    nblk = N // bs
+    rows = np.unique(np.linspace(0, nblk - 1, rows_wanted).astype(np.int64))
+    t0 = time.perf_counter()
+    qp = osel.pool_mean_tok_then_heads(qh, bs, "bf16")
+    kp = osel.pool_mean_tok_then_heads(kh, bs, "bf16")
+    t_pool = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    raw = osel.scores(qp, kp, "bf16", "dot", rows=rows)
+    sel = osel.select_conv_a(raw, topk, True, rows=rows)
+    t_sel = time.perf_counter() - t0
+    full_sel = np.zeros((B, nblk, sel.shape[-1]), dtype=np.int64)
+    full_sel[:, rows] = sel
+    t0 = time.perf_counter()
+    oattn.fwd(qh, kh, vh, full_sel[:, None], "slot_causal", rows=rows)
+    t_fwd = time.perf_counter() - t0
+    scale = nblk / len(rows)
+    total = t_pool + (t_sel + t_fwd) * scale
+    return {
+        "value": B * N / total, "unit": "tokens/s", "cores": 1, "kind": "port",
+        "sample": (f"numpy float64 oracle: full q/k pooling ({t_pool:.2f} s) + scores, top-k and "
+                   f"gather attention for {len(rows)} of {nblk} query blocks x {H} heads "
+                   f"({t_sel + t_fwd:.2f} s), scaled x{scale:.1f} to all blocks; "
+                   f"est. {total:.1f} s per step"),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from fbsa_amd import ops, selection
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    B, H, N, D, bs, topk = 1, a.H, a.N, a.D, a.bs, a.topk
+    nblk = N // bs
+    kk = 1 + min(topk, nblk - 1)
+    g = torch.Generator(device=dev).manual_seed(0)
+    sc = D ** -0.5
+    q, k, v = ((torch.randn(B, H, N, D, generator=g, device=dev) * sc).to(torch.bfloat16) for _ in range(3))
+    do = torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16) if a.bwd else None
+
+    stream = torch.cuda.current_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    fwd_ms, sel_ms = [], []
+
+    def step(timed):
+        e0, e1, e2 = ev(), ev(), ev()
+        e0.record(stream)
+        sel = selection.select_mean_pooled(q, k, bs, topk, causal=True)
+        e1.record(stream)
+        o, lse = ops.attention_forward(q, k, v, sel[:, None], mask=ops.MASK_SLOT_CAUSAL, need_lse=True)
+        e2.record(stream)
+        if timed:
+            sel_ms.append((e0, e1))
+            fwd_ms.append((e1, e2))
+        return sel, o, lse
+
+    for _ in range(a.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / a.steps
+    t_sel = sum(x.elapsed_time(y) for x, y in sel_ms) / a.steps
+    t_fwd = sum(x.elapsed_time(y) for x, y in fwd_ms) / a.steps
+
+    flops = 4.0 * B * H * nblk * kk * bs * bs * D
+    achieved = flops / (t_fwd * 1e-3) / 1e12
+    wl = f"cfg3_N{N}_H{H}_D{D}_bs{bs}_top{topk}"
+    gathered = B * H * nblk * kk * 2 * bs * D * 2
+    out = {
+        "metric": "select+fwd tokens/s at 262k tokens, 1 GPU (bf16, H8 D64 bs64 top-16, causal)",
+        "value": B * N / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (q,k,v ~ N(0,1)/sqrt(D), seed 0, device generator)",
+        "config": {"workload": "BASELINE configs[2]: block-pair selection (mean-pooled q.k, top-16, "
+                               "own-first) + fused block-sparse forward, causal",
+                   "B": B, "H": H, "N": N, "D": D, "block": bs, "nblk": nblk, "topk": topk, "kk": kk},
+        "ms_select": t_sel, "ms_fwd": t_fwd,
+        "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": traffic_from_profiles("fwd_kernel", wl), "kernel": "fbsa::fwd_kernel<bf16,64,64>",
+                     "flop_per_launch": flops},
+        "strict_roofline_select_fwd_us": None,
+    }
+    # strict roofline of the whole select+fwd step: selection reads q,k once (HBM), forward FLOPs (MFMA)
+    t_star = (2 * B * H * N * D * 2) / (PEAK_HBM_GBS * 1e9) + flops / (PEAK_BF16_TFLOPS * 1e12)
+    out["strict_roofline_select_fwd_us"] = t_star * 1e6
+    out["frac_of_strict_roofline"] = t_star / (ms_step * 1e-3)
+
+    if a.bwd:
+        from fbsa_amd import autograd  # noqa: F401
+        bwd_ev = []
+        sel, o, lse = step(False)
+        for it in range(a.warmup + a.steps):
+            e0, e1 = ev(), ev()
+            e0.record(stream)
+            ops.attention_backward(q, k, v, sel[:, None], o, lse, do, mask=ops.MASK_SLOT_CAUSAL)
+            e1.record(stream)
+            if it >= a.warmup:
+                bwd_ev.append((e0, e1))
+        torch.cuda.synchronize()
+        t_bwd = sum(x.elapsed_time(y) for x, y in bwd_ev) / a.steps
+        bflops = 2.5 * flops
+        out["ms_bwd"] = t_bwd
+        out["bwd_TFLOPs"] = bflops / (t_bwd * 1e-3) / 1e12
+        out["train_step_tokens_per_s"] = B * N / ((ms_step + t_bwd) * 1e-3)
+
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(q, k, v, bs, topk, a.cpu_rows)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -8,6 +8,7 @@ import torch
 
 from . import _lib
 
+MASK_NONE, MASK_SLOT_CAUSAL, MASK_TOKEN_CAUSAL = _lib.MASK_NONE, _lib.MASK_SLOT_CAUSAL, _lib.MASK_TOKEN_CAUSAL
 SUPPORTED_D = (32, 64, 128, 256)
 SUPPORTED_BS = (16, 32, 64, 128)
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}

@@ -1,0 +1,97 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and rejects bad arguments on the host before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from fbsa_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "fbsa.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(fbsa_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert "fbsa_fwd" in names and "fbsa_select" in names and "fbsa_bwd" in names
+    for n in names:
+        assert hasattr(lib, n), f"libfbsa.so does not export {n}"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with include/fbsa.h"
+
+
+def test_struct_layout_matches_header():
+    # int32 dtype/mask, 10 int64 sizes, float scale + int32 flags, 6 x 3 int64 strides
+    assert ctypes.sizeof(_lib.AttnDesc) == 8 + 10 * 8 + 8 + 18 * 8
+    assert ctypes.sizeof(_lib.PoolDesc) == 8 + 8 * 8 + 3 * 8
+    assert ctypes.sizeof(_lib.SelectDesc) == 6 * 4 + 6 * 8
+
+
+def _desc(**kw):
+    d = _lib.AttnDesc()
+    d.dtype, d.mask = _lib.BF16, _lib.MASK_SLOT_CAUSAL
+    d.B, d.Hq, d.Hkv, d.L, d.D, d.bs, d.nblk, d.kk, d.hsel, d.l_valid = 1, 2, 2, 256, 64, 64, 4, 3, 1, 256
+    d.scale = 0.125
+    for s in ("sq", "sk", "sv", "so", "sdo", "sog"):
+        getattr(d, s)[:] = (2 * 256 * 64, 256 * 64, 64)
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+DUMMY = 1 << 20  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("bs", 48, "block size"),
+    ("D", 80, "head dim"),
+    ("L", 250, "nblk*bs"),
+    ("Hkv", 3, "multiple"),
+    ("hsel", 3, "hsel"),
+    ("l_valid", 0, "l_valid"),
+    ("dtype", 7, "dtype"),
+    ("mask", 9, "mask"),
+    ("kk", 0, "positive"),
+])
+def test_fwd_rejects_bad_descriptor(field, value, needle):
+    lib = _lib.load()
+    d = _desc(**{field: value})
+    st = lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, DUMMY, None, None, DUMMY, None, None)
+    assert st in (_lib.EINVAL, _lib.EUNSUPPORTED)
+    assert needle in lib.fbsa_last_error().decode()
+
+
+def test_fwd_rejects_null_and_misaligned_pointers():
+    lib = _lib.load()
+    d = _desc()
+    assert lib.fbsa_fwd(d, None, DUMMY, DUMMY, DUMMY, None, None, DUMMY, None, None) == _lib.EINVAL
+    assert lib.fbsa_fwd(d, DUMMY + 2, DUMMY, DUMMY, DUMMY, None, None, DUMMY, None, None) == _lib.EINVAL
+    assert "aligned" in lib.fbsa_last_error().decode()
+    d.sq[2] = 65  # row stride not a multiple of 16 bytes
+    assert lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, DUMMY, None, None, DUMMY, None, None) == _lib.EINVAL
+
+
+def test_select_rejects_bad_budget():
+    lib = _lib.load()
+    d = _lib.SelectDesc()
+    d.dtype, d.score, d.convention, d.causal = _lib.BF16, _lib.SCORE_DOT, _lib.SEL_OWN_FIRST, 1
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = 1, 1, 64, 64, 8, 8   # convention A needs kk = 9
+    assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EINVAL
+    assert "kk" in lib.fbsa_last_error().decode()
+    d.kk, d.topk = 64, 63
+    assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EUNSUPPORTED
+
+
+def test_python_ops_require_gpu_tensors():
+    import torch
+    from fbsa_amd import ops
+    q = torch.zeros(1, 1, 64, 64, dtype=torch.bfloat16)
+    sel = torch.zeros(1, 1, 1, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.attention_forward(q, q, q, sel, mask=ops.MASK_SLOT_CAUSAL)
