@@ -143,28 +143,111 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
 
 }  // extern "C"
 
-// ---- entry points not implemented yet: report FBSA_EUNSUPPORTED ----
+// ---- backward ----
+namespace fbsa {
+
+static int check_bwd(const fbsa_attn_desc *d, const char *fn, BwdLayout *lay, const void *ws, size_t ws_bytes) {
+  int e = check_attn(d, fn);
+  if (e) return e;
+  if (d->flags & ~FBSA_FLAG_OUT_GATE) return fail(FBSA_EINVAL, "%s: unknown flags 0x%x", fn, d->flags);
+  e = bwd_layout(d, lay);
+  if (e) return e;
+  if (!ws || !aligned(ws, 256)) return fail(FBSA_EINVAL, "%s: workspace must be non-null and 256-byte aligned", fn);
+  if (ws_bytes < lay->total)
+    return fail(FBSA_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, lay->total);
+  return FBSA_OK;
+}
+
+static int check_dout(const fbsa_attn_desc *d, const void *dout, const char *fn) {
+  if (d->flags & FBSA_FLAG_OUT_GATE) return FBSA_OK;  // the stages read the workspace copy
+  if (!dout || !aligned(dout, 16)) return fail(FBSA_EINVAL, "%s: dout must be non-null and 16-byte aligned", fn);
+  const int64_t es = esize(d->dtype);
+  for (int x = 0; x < 3; ++x)
+    if (d->sdo[x] < 0 || (d->sdo[x] * es) % 16)
+      return fail(FBSA_EINVAL, "%s: dout stride[%d] must be a non-negative multiple of 16 bytes", fn, x);
+  return FBSA_OK;
+}
+
+static int check_qkv(const void *q, const void *k, const void *v, const char *fn) {
+  if (!q || !k || !v) return fail(FBSA_EINVAL, "%s: null q/k/v", fn);
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16)) return fail(FBSA_EINVAL, "%s: q/k/v must be 16-byte aligned", fn);
+  return FBSA_OK;
+}
+
+}  // namespace fbsa
+
 extern "C" {
-int fbsa_bwd_prep(const fbsa_attn_desc *, const void *, const void *, float *, void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_prep: not implemented");
+
+size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *d) {
+  BwdLayout lay;
+  if (check_attn(d, "fbsa_bwd_workspace_bytes")) return 0;
+  if (bwd_layout(d, &lay)) return 0;
+  return lay.total;
 }
-size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *) { return 0; }
-int fbsa_transpose_index(const fbsa_attn_desc *, const int32_t *, void *, size_t, void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_transpose_index: not implemented");
+
+int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, const float *lse, const void *out_gate,
+                  void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_bwd_prep", &lay, workspace, workspace_bytes);
+  if (e) return e;
+  const bool og = (d->flags & FBSA_FLAG_OUT_GATE) != 0;
+  if (og != (out_gate != nullptr) || og != (dout_gate != nullptr))
+    return fail(FBSA_EINVAL, "fbsa_bwd_prep: out_gate and dout_gate must be given exactly when FBSA_FLAG_OUT_GATE is set");
+  if (!o || !dout || !lse || !aligned(o, 16) || !aligned(dout, 16) || !aligned(lse, 4))
+    return fail(FBSA_EINVAL, "fbsa_bwd_prep: o/dout (16-byte aligned) and lse must be non-null");
+  const int64_t es = esize(d->dtype);
+  for (int x = 0; x < 3; ++x)
+    if (d->sdo[x] < 0 || (d->sdo[x] * es) % 16)
+      return fail(FBSA_EINVAL, "fbsa_bwd_prep: dout stride[%d] must be a non-negative multiple of 16 bytes", x);
+  if (og && (!aligned(out_gate, es) || !aligned(dout_gate, 16)))
+    return fail(FBSA_EINVAL, "fbsa_bwd_prep: out_gate / dout_gate misaligned");
+  return run_bwd_prep(d, lay, o, dout, lse, out_gate, dout_gate, (char *)workspace, (hipStream_t)stream);
 }
-int fbsa_bwd_dq(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const void *,
-                const float *, const float *, const int32_t *, const float *, const void *, void *, float *, void *,
-                void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_dq: not implemented");
+
+int fbsa_transpose_index(const fbsa_attn_desc *d, const int32_t *sel, void *workspace, size_t workspace_bytes,
+                         void *stream) {
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_transpose_index", &lay, workspace, workspace_bytes);
+  if (e) return e;
+  if (!sel || !aligned(sel, 4)) return fail(FBSA_EINVAL, "fbsa_transpose_index: sel must be non-null and 4-byte aligned");
+  return run_transpose_index(d, lay, sel, (char *)workspace, (hipStream_t)stream);
 }
-int fbsa_bwd_dkdv(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const float *,
-                  const float *, const int32_t *, const float *, const void *, const void *, size_t, void *, void *,
-                  void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_dkdv: not implemented");
+
+int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *dout,
+                const int32_t *sel, const float *gate, void *dq, float *dgate, void *workspace, size_t workspace_bytes,
+                void *stream) {
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_bwd_dq", &lay, workspace, workspace_bytes);
+  if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dq");
+  if (!e) e = check_dout(d, dout, "fbsa_bwd_dq");
+  if (e) return e;
+  if (!sel || !aligned(sel, 4) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned (sel non-null)");
+  if (!dq || !aligned(dq, 16)) return fail(FBSA_EINVAL, "fbsa_bwd_dq: dq must be non-null and 16-byte aligned");
+  return run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, (char *)workspace, (hipStream_t)stream);
 }
-int fbsa_bwd(const fbsa_attn_desc *, const void *, const void *, const void *, const void *, const void *,
-             const float *, const int32_t *, const float *, const void *, void *, void *, void *, float *, void *,
-             void *, size_t, void *) {
-  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: not implemented");
+
+int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *dout,
+                  const float *gate, void *dk, void *dv, void *workspace, size_t workspace_bytes, void *stream) {
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_bwd_dkdv", &lay, workspace, workspace_bytes);
+  if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dkdv");
+  if (!e) e = check_dout(d, dout, "fbsa_bwd_dkdv");
+  if (e) return e;
+  if (gate && !aligned(gate, 4)) return fail(FBSA_EINVAL, "fbsa_bwd_dkdv: gate must be 4-byte aligned");
+  if (!dk || !dv || !aligned(dk, 16) || !aligned(dv, 16))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dkdv: dk/dv must be non-null and 16-byte aligned");
+  return run_bwd_dkdv(d, lay, q, k, v, dout, gate, dk, dv, (char *)workspace, (hipStream_t)stream);
 }
+
+int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o, const void *dout,
+             const float *lse, const int32_t *sel, const float *gate, const void *out_gate, void *dq, void *dk,
+             void *dv, float *dgate, void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
+  int e = fbsa_bwd_prep(d, o, dout, lse, out_gate, dout_gate, workspace, workspace_bytes, stream);
+  if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
+  if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);
+  if (!e) e = fbsa_bwd_dkdv(d, q, k, v, dout, gate, dk, dv, workspace, workspace_bytes, stream);
+  return e;
 }
+
+}  // extern "C"

@@ -1,0 +1,690 @@
+// Backward of the fused block-sparse attention for gfx950 (CDNA4).
+//
+// Four stages, none of them with floating-point atomics (results are bitwise
+// repeatable):
+//   1. prep_kernel     per query row: delta = sum_d dO*O and lse*log2(e)
+//                      (rowstat); with an output gate also dO*sigmoid(g) and
+//                      the gate gradient dO*O*(1 - sigmoid(g)).
+//   2. keys_kernel + stable radix sort + seg_off_kernel
+//                      the block-transposed index: for each (b, hsel, key
+//                      block j) the valid (i, slot) pairs that read block j,
+//                      ascending, as a CSR.
+//   3. dq_kernel       one workgroup per (b, query head, query block i), one
+//                      wave per 16 query rows, walking i's selected key blocks
+//                      (K and V through a direct-to-LDS ring, as in the
+//                      forward): S^T = K Q^T and dP^T = V dO^T on MFMA,
+//                      P = exp2(S*scale*log2e + gate*log2e - lse*log2e),
+//                      dS = P (dP - delta), dQ^T += K^T dS^T; optional per-head
+//                      gate-gradient partials sum(dS) per slot.
+//   4. dkdv_kernel     one workgroup per (b, KV head, key block j), one wave
+//                      per 16 keys held in registers, walking j's transposed
+//                      list (times the GQA group's query heads): Q and dO
+//                      tiles of the reading query block through the ring,
+//                      S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+//
+// Reference semantics: src/triton_kernel.py:77-181 (recompute of P from the
+// same scores, the slot-0 triu / future-content masks, gate after scale,
+// dS = P (dP - D), dQ = dS K scale, dK = dS^T Q scale, dV = P^T dO), the
+// token-causal/padding/duplicate masks of src/qwen_blocksparse.py:67-72, and
+// the gate gradient the gather path (src/ssa_model.py:72-74) gives.
+#include <hipcub/hipcub.hpp>
+
+#include "fbsa_common.h"
+#include "fbsa_internal.h"
+#include "fbsa_tiles.h"
+
+namespace fbsa {
+
+enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2 };
+
+#ifndef FBSA_DQ_LDS_BUDGET
+#define FBSA_DQ_LDS_BUDGET 32768
+#endif
+#ifndef FBSA_DKDV_LDS_BUDGET
+#define FBSA_DKDV_LDS_BUDGET 61440
+#endif
+
+static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// ----------------------------------------------------------------- layout
+int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
+  lay->n = d->B * d->hsel * d->nblk * d->kk;
+  lay->nseg = d->B * d->hsel * d->nblk;
+  if (d->nblk * d->kk >= 0x7fffffffLL || lay->nseg >= 0x7fffffffLL || lay->n >= 0x7fffffffLL)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: selection too large for the 32-bit transposed index");
+  int bits = 1;
+  while (((int64_t)1 << bits) <= lay->nseg) ++bits;
+  lay->end_bit = bits;
+  size_t tmp = 0;
+  hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, tmp, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+                                                    (const int32_t *)nullptr, (int32_t *)nullptr, (int)lay->n, 0,
+                                                    bits, (hipStream_t)0);
+  if (e != hipSuccess) return hip_check(e, "radix sort workspace query");
+  lay->sort_tmp_bytes = tmp;
+  const size_t rows = (size_t)(d->B * d->Hq * d->L);
+  size_t off = 0;
+  lay->rowstat = off; off = al256(off + rows * 8);
+  lay->dout_attn = off;
+  if (d->flags & FBSA_FLAG_OUT_GATE) off = al256(off + rows * (size_t)d->D * (size_t)esize(d->dtype));
+  lay->dgate_part = off; off = al256(off + (size_t)(d->B * d->Hq * d->nblk * d->kk) * 4);
+  lay->keys_in = off; off = al256(off + (size_t)lay->n * 4);
+  lay->keys_out = off; off = al256(off + (size_t)lay->n * 4);
+  lay->vals_in = off; off = al256(off + (size_t)lay->n * 4);
+  lay->vals_out = off; off = al256(off + (size_t)lay->n * 4);
+  lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
+  lay->sort_tmp = off; off = al256(off + tmp);
+  lay->total = off;
+  return FBSA_OK;
+}
+
+// ----------------------------------------------------------------- stage 1
+struct PrepArgs {
+  const void *o, *dout, *og;
+  const float *lse;
+  float2 *rowstat;
+  void *dout_attn, *dout_gate;
+  int64_t Hq, L, rows;
+  int64_t so[3], sdo[3], sog[3];
+};
+
+template <typename T> __device__ __forceinline__ float half_to_f32(uint32_t h) {
+  if constexpr (__is_same(T, bf16)) {
+    return __uint_as_float(h << 16);
+  } else {
+    const unsigned short hs = (unsigned short)h;
+    _Float16 x;
+    __builtin_memcpy(&x, &hs, 2);
+    return (float)x;
+  }
+}
+
+template <typename T> __device__ __forceinline__ void load8f(const T *p, float *v) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[4 + e] = b[e]; }
+  } else {
+    // 32-bit words split with shifts: bit-casting elements of a 16-bit vector
+    // value one by one is miscompiled (every element reads element 0).
+    const uint4 r = *(const uint4 *)p;
+    const uint32_t wd[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = half_to_f32<T>(wd[e] & 0xFFFFu);
+      v[2 * e + 1] = half_to_f32<T>(wd[e] >> 16);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+  constexpr int TPR = D / 8;  // threads per row, 8 elements each
+  constexpr int RPB = 256 / TPR;
+  const int tid = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
+  const int c = tid % TPR;
+  float acc = 0.f;
+  if (row < a.rows) {
+    const int64_t t = row % a.L, bh = row / a.L, h = bh % a.Hq, b = bh / a.Hq;
+    float ov[8], dv[8];
+    load8f<T>((const T *)a.o + b * a.so[0] + h * a.so[1] + t * a.so[2] + 8 * c, ov);
+    load8f<T>((const T *)a.dout + b * a.sdo[0] + h * a.sdo[1] + t * a.sdo[2] + 8 * c, dv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(ov[e], dv[e], acc);
+    if (a.og) {
+      const T *grow = (const T *)a.og + b * a.sog[0] + h * a.sog[1] + t * a.sog[2] + 8 * c;
+      T *da = (T *)a.dout_attn + row * D + 8 * c;
+      T *dg = (T *)a.dout_gate + row * D + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float s = 1.f / (1.f + __expf(-(float)grow[e]));
+        da[e] = (T)(dv[e] * s);
+        dg[e] = (T)(dv[e] * ov[e] * (1.f - s));
+      }
+    }
+  }
+#pragma unroll
+  for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (row < a.rows && c == 0) {
+    const float l = a.lse[row];
+    a.rowstat[row] = make_float2(l == -INFINITY ? INFINITY : l * kLog2e, acc);
+  }
+}
+
+template <typename T, int D> static void launch_prep(const PrepArgs &a, hipStream_t s) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t nwg = (a.rows + RPB - 1) / RPB;
+  hipLaunchKernelGGL((prep_kernel<T, D>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+}
+
+template <typename T> static int prep_d(const PrepArgs &a, int64_t D, hipStream_t s) {
+  switch (D) {
+    case 32: launch_prep<T, 32>(a, s); break;
+    case 64: launch_prep<T, 64>(a, s); break;
+    case 128: launch_prep<T, 128>(a, s); break;
+    case 256: launch_prep<T, 256>(a, s); break;
+    default: return fail(FBSA_EUNSUPPORTED, "fbsa_bwd_prep: head dim %lld", (long long)D);
+  }
+  return hip_check(hipGetLastError(), "prep_kernel launch");
+}
+
+int run_bwd_prep(const fbsa_attn_desc *d, const BwdLayout &lay, const void *o, const void *dout, const float *lse,
+                 const void *out_gate, void *dout_gate, char *ws, hipStream_t s) {
+  PrepArgs a;
+  a.o = o; a.dout = dout; a.og = out_gate; a.lse = lse;
+  a.rowstat = (float2 *)(ws + lay.rowstat);
+  a.dout_attn = ws + lay.dout_attn;
+  a.dout_gate = dout_gate;
+  a.Hq = d->Hq; a.L = d->L; a.rows = d->B * d->Hq * d->L;
+  for (int x = 0; x < 3; ++x) { a.so[x] = d->so[x]; a.sdo[x] = d->sdo[x]; a.sog[x] = d->sog[x]; }
+  switch (d->dtype) {
+    case FBSA_BF16: return prep_d<bf16>(a, d->D, s);
+    case FBSA_F16: return prep_d<f16>(a, d->D, s);
+    default: return prep_d<float>(a, d->D, s);
+  }
+}
+
+// ----------------------------------------------------------------- stage 2
+struct IdxArgs {
+  const int32_t *sel;
+  uint32_t *keys;
+  int32_t *vals;
+  int64_t nblk, kk, n, nseg, bs, l_valid;
+  int mask;
+};
+
+// One thread per (b, hsel, i, slot): key = CSR segment of the slot's block
+// when the slot is valid under the mask rule, nseg (sorted last) otherwise.
+__global__ __launch_bounds__(256) void keys_kernel(IdxArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.n) return;
+  const int64_t s = e % a.kk, r = e / a.kk, i = r % a.nblk, bhs = r / a.nblk;
+  const int32_t *row = a.sel + r * a.kk;
+  const int64_t j = row[s];
+  const bool inb = j >= 0 && j < a.nblk;
+  bool valid;
+  if (a.mask == FBSA_MASK_NONE) valid = inb;
+  else if (a.mask == FBSA_MASK_SLOT_CAUSAL) valid = s == 0 ? inb : (inb && j < i);
+  else {
+    valid = inb && j <= i && j * a.bs < a.l_valid;
+    for (int64_t s2 = 0; s2 < s && valid; ++s2) valid = row[s2] != j;
+  }
+  a.keys[e] = valid ? (uint32_t)(bhs * a.nblk + j) : (uint32_t)a.nseg;
+  a.vals[e] = (int32_t)(i * a.kk + s);
+}
+
+// seg_off[x] = first sorted position whose key is >= x, for x in [0, nseg].
+__global__ __launch_bounds__(256) void seg_off_kernel(const uint32_t *keys, int64_t n, int64_t nseg, int32_t *seg_off) {
+  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (x > nseg) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)keys[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  seg_off[x] = (int32_t)lo;
+}
+
+int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int32_t *sel, char *ws, hipStream_t s) {
+  IdxArgs a;
+  a.sel = sel;
+  a.keys = (uint32_t *)(ws + lay.keys_in);
+  a.vals = (int32_t *)(ws + lay.vals_in);
+  a.nblk = d->nblk; a.kk = d->kk; a.n = lay.n; a.nseg = lay.nseg; a.bs = d->bs; a.l_valid = d->l_valid;
+  a.mask = d->mask;
+  hipLaunchKernelGGL(keys_kernel, dim3((unsigned)((lay.n + 255) / 256)), dim3(256), 0, s, a);
+  int e = hip_check(hipGetLastError(), "keys_kernel launch");
+  if (e) return e;
+  size_t tmp = lay.sort_tmp_bytes;
+  e = hip_check(hipcub::DeviceRadixSort::SortPairs(ws + lay.sort_tmp, tmp, (const uint32_t *)(ws + lay.keys_in),
+                                                   (uint32_t *)(ws + lay.keys_out), (const int32_t *)(ws + lay.vals_in),
+                                                   (int32_t *)(ws + lay.vals_out), (int)lay.n, 0, lay.end_bit, s),
+                "radix sort of the transposed index");
+  if (e) return e;
+  hipLaunchKernelGGL(seg_off_kernel, dim3((unsigned)((lay.nseg + 1 + 255) / 256)), dim3(256), 0, s,
+                     (const uint32_t *)(ws + lay.keys_out), lay.n, lay.nseg, (int32_t *)(ws + lay.seg_off));
+  return hip_check(hipGetLastError(), "seg_off_kernel launch");
+}
+
+// ----------------------------------------------------------------- stages 3, 4
+struct BwdArgs {
+  const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
+  const float2 *rowstat;
+  const int32_t *sel;
+  const float *gate;
+  void *dq, *dk, *dv;
+  float *dgate_part;
+  const int32_t *seg_off, *ent;
+  int64_t B, Hq, Hkv, L, nblk, kk, hsel, l_valid;
+  int64_t sq[3], sk[3], sv[3], sdo[3];
+  float scale2, scale;
+  int mask, grp;
+};
+
+template <typename T, int BS, int D, int BUDGET, int META> struct BwdCfg {
+  static constexpr int ES = sizeof(T);
+  static constexpr int NW = BS / 16;
+  static constexpr int NT = NW * 64;
+  static constexpr int KC = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
+  static constexpr int NCH = BS / KC;
+  static constexpr int CPR = D * ES / 16;
+  static constexpr int TILE_BYTES = KC * D * ES;
+  static constexpr int META_BYTES = META ? NW * KC * 8 : 0;  // per-wave copies of (lse2, delta) rows
+  static constexpr int STAGE_BYTES = 2 * TILE_BYTES + META_BYTES;
+  static constexpr int LPT = 2 * TILE_BYTES / (NT * 16);
+  static constexpr int NS0 = BUDGET / STAGE_BYTES;
+  static constexpr int NSTAGE = NS0 < 2 ? 2 : (NS0 > 4 ? 4 : NS0);
+  static_assert(LPT * NT * 16 == 2 * TILE_BYTES, "stage must split evenly over threads");
+  static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
+};
+
+template <typename T, int BS, int D>
+__global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
+  using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char *stages = smem;
+  int *s_blk = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
+  int *s_kind = s_blk + a.kk;
+  float *s_gate = (float *)(s_kind + a.kk);
+  int *s_cidx = (int *)(s_gate + a.kk);
+  float *s_dg = (float *)(s_cidx + a.kk);  // [NW][kk], indexed by compact slot
+  __shared__ int s_nvalid;
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
+  const int64_t total = a.B * a.Hq * a.nblk;
+  int64_t t = xcd_remap(blockIdx.x, total);
+  const int hin = (int)(t % a.grp); t /= a.grp;
+  const int64_t i = t % a.nblk; t /= a.nblk;
+  const int hk = (int)(t % a.Hkv);
+  const int64_t b = t / a.Hkv;
+  const int hq = hk * a.grp + hin;
+  const int hs = a.hsel == 1 ? 0 : hk;
+
+  // plan: compact list of valid slots (same rule as the forward)
+  const int64_t rowoff = ((b * a.hsel + hs) * a.nblk + i) * a.kk;
+  const int32_t *selrow = a.sel + rowoff;
+  if (w == 0) {
+    int nout = 0;
+    for (int s0 = 0; s0 < a.kk; s0 += 64) {
+      const int s = s0 + lane;
+      bool valid = false;
+      int kind = KIND_FULL, j = 0;
+      if (s < a.kk) {
+        j = selrow[s];
+        const bool inb = j >= 0 && j < a.nblk;
+        if (a.mask == FBSA_MASK_NONE) {
+          valid = inb;
+        } else if (a.mask == FBSA_MASK_SLOT_CAUSAL) {
+          if (s == 0) { valid = inb; kind = KIND_DIAG; }
+          else valid = inb && j < i;
+        } else {
+          valid = inb && j <= i && (int64_t)j * BS < a.l_valid;
+          for (int s2 = 0; s2 < s && valid; ++s2) valid = selrow[s2] != j;
+          if (valid && (j == i || (int64_t)(j + 1) * BS > a.l_valid)) kind = KIND_ABS;
+        }
+      }
+      const uint64_t m = __ballot(valid);
+      const int pos = nout + __popcll(m & ((1ull << lane) - 1ull));
+      if (s < a.kk) s_cidx[s] = valid ? pos : -1;
+      if (valid) {
+        s_blk[pos] = j;
+        s_kind[pos] = kind;
+        s_gate[pos] = a.gate ? a.gate[rowoff + s] * kLog2e : 0.f;
+      }
+      nout += __popcll(m);
+    }
+    if (lane == 0) s_nvalid = nout;
+  }
+
+  const int tq = w * 16 + p;
+  const int64_t qpos = i * BS + tq;
+  RowFrag<T, D> qf, df;
+  qf.load((const T *)a.q + b * a.sq[0] + hq * a.sq[1] + qpos * a.sq[2], g);
+  df.load((const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1] + qpos * a.sdo[2], g);
+  const float2 rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
+  const float lse2 = rs.x, delta = rs.y;
+  __syncthreads();
+  const int nv = s_nvalid;
+  const int nchunks = nv * C::NCH;
+
+  const T *kbase = (const T *)a.k + b * a.sk[0] + hk * a.sk[1];
+  const T *vbase = (const T *)a.v + b * a.sv[0] + hk * a.sv[1];
+  auto issue = [&](int c) {
+    const int slot = c / C::NCH, ch = c % C::NCH;
+    const int64_t row0 = (int64_t)s_blk[slot] * BS + ch * C::KC;
+    issue_tile_pair<T, C::KC, D, C::NW, C::LPT>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2], vbase,
+                                                a.sv[2], row0, w, lane);
+  };
+
+  f32x4 dqacc[D / 16];
+#pragma unroll
+  for (int mt = 0; mt < D / 16; ++mt) dqacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dgl = 0.f;
+  const bool want_dg = a.dgate_part != nullptr;
+
+#pragma unroll
+  for (int c = 0; c < C::NSTAGE - 1; ++c)
+    if (c < nchunks) issue(c);
+
+  for (int c = 0; c < nchunks; ++c) {
+    if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+    const int ahead = nchunks - 1 - c;
+    wait_ring<C::LPT>(ahead < C::NSTAGE - 1 ? ahead : C::NSTAGE - 1);
+    lds_barrier();
+
+    const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
+    const char *Vs = Ks + C::TILE_BYTES;
+    const int slot = c / C::NCH, ch = c % C::NCH;
+    const int kind = s_kind[slot];
+    const float gt = s_gate[slot];
+    const int64_t j = s_blk[slot];
+
+    f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
+    mm_rows_frag<T, D, C::KC / 16>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
+    mm_rows_frag<T, D, C::KC / 16>(Vs, df, dpacc, g, p);  // dP^T
+
+    int lim = 1 << 30;
+    if (kind != KIND_FULL) {
+      const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
+                                              : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
+                                                                                            : a.l_valid - j * BS - 1);
+      lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
+    }
+    const float off = gt - lse2;
+    float ds[C::KC / 16][4];
+#pragma unroll
+    for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = (16 * m + r <= lim) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off)) : 0.f;
+        ds[m][r] = pv * (dpacc[m][r] - delta);
+        dgl += ds[m][r];
+      }
+    if (want_dg && ch == C::NCH - 1) {
+#pragma unroll
+      for (int x = 1; x < 64; x <<= 1) dgl += shfl_xor_f(dgl, x);
+      if (lane == 0) s_dg[w * a.kk + slot] = dgl;
+      dgl = 0.f;
+    }
+    mm_tr_acc<T, D, C::KC>(Ks, ds, dqacc, g, p);  // dQ^T += K^T dS^T
+    lds_barrier();
+  }
+
+  T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
+#pragma unroll
+  for (int mt = 0; mt < D / 16; ++mt) {
+    const int d0 = 16 * mt + 4 * g;
+    if constexpr (sizeof(T) == 4) {
+      *(f32x4 *)(dqrow + d0) = f32x4{dqacc[mt][0] * a.scale, dqacc[mt][1] * a.scale, dqacc[mt][2] * a.scale,
+                                     dqacc[mt][3] * a.scale};
+    } else {
+      s16x4 pk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)(dqacc[mt][r] * a.scale));
+      *(s16x4 *)(dqrow + d0) = pk;
+    }
+  }
+  if (want_dg) {
+    __syncthreads();
+    float *dst = a.dgate_part + ((b * a.Hq + hq) * a.nblk + i) * a.kk;
+    for (int s = tid; s < a.kk; s += C::NT) {
+      const int ci = s_cidx[s];
+      float v = 0.f;
+      if (ci >= 0)
+        for (int ww = 0; ww < C::NW; ++ww) v += s_dg[ww * a.kk + ci];
+      dst[s] = v;
+    }
+  }
+}
+
+template <typename T, int BS, int D>
+__global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
+  using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
+  constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char *stages = smem;
+  int *s_i = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
+  int *s_kind = s_i + MAXE;
+  float *s_gate = (float *)(s_kind + MAXE);
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
+  const int64_t total = a.B * a.Hkv * a.nblk;
+  int64_t t = xcd_remap(blockIdx.x, total);
+  const int64_t j = t % a.nblk; t /= a.nblk;
+  const int hk = (int)(t % a.Hkv);
+  const int64_t b = t / a.Hkv;
+  const int hs = a.hsel == 1 ? 0 : hk;
+  const int64_t seg = (b * a.hsel + hs) * a.nblk + j;
+  const int e0 = a.seg_off[seg], e1 = a.seg_off[seg + 1];
+
+  const int u = w * 16 + p;  // this lane's key row within block j (B-operand column)
+  const int64_t kpos = j * BS + u;
+  RowFrag<T, D> kf, vf;
+  kf.load((const T *)a.k + b * a.sk[0] + hk * a.sk[1] + kpos * a.sk[2], g);
+  vf.load((const T *)a.v + b * a.sv[0] + hk * a.sv[1] + kpos * a.sv[2], g);
+  const bool keyok = kpos < a.l_valid;
+
+  f32x4 dkacc[D / 16], dvacc[D / 16];
+#pragma unroll
+  for (int mt = 0; mt < D / 16; ++mt) {
+    dkacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dvacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int eb = e0; eb < e1; eb += MAXE) {
+    const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
+    __syncthreads();  // the previous batch's entries are no longer read
+    for (int x = tid; x < ne; x += C::NT) {
+      const int ev = a.ent[eb + x];
+      const int i = (int)(ev / a.kk), s = (int)(ev % a.kk);
+      int kind = KIND_FULL;
+      if (a.mask == FBSA_MASK_SLOT_CAUSAL) kind = s == 0 ? KIND_DIAG : KIND_FULL;
+      else if (a.mask == FBSA_MASK_TOKEN_CAUSAL)
+        kind = (j == i || (j + 1) * BS > a.l_valid) ? KIND_ABS : KIND_FULL;
+      s_i[x] = i;
+      s_kind[x] = kind;
+      s_gate[x] = a.gate ? a.gate[((b * a.hsel + hs) * a.nblk + i) * a.kk + s] * kLog2e : 0.f;
+    }
+    __syncthreads();
+    const int nchunks = ne * a.grp * C::NCH;
+    auto issue = [&](int c) {
+      const int task = c / C::NCH, ch = c % C::NCH;
+      const int x = task / a.grp, hq = hk * a.grp + task % a.grp;
+      const int64_t row0 = (int64_t)s_i[x] * BS + ch * C::KC;
+      char *st = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
+      issue_tile_pair<T, C::KC, D, C::NW, C::LPT>(st, (const T *)a.q + b * a.sq[0] + hq * a.sq[1], a.sq[2],
+                                                  (const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1], a.sdo[2], row0,
+                                                  w, lane);
+      if (lane < C::KC / 2)
+        g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + 2 * lane, st + 2 * C::TILE_BYTES + w * (C::KC * 8));
+    };
+#pragma unroll
+    for (int c = 0; c < C::NSTAGE - 1; ++c)
+      if (c < nchunks) issue(c);
+
+    for (int c = 0; c < nchunks; ++c) {
+      if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+      const int ahead = nchunks - 1 - c;
+      wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 1 ? ahead : C::NSTAGE - 1);
+      lds_barrier();
+
+      const char *Qs = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
+      const char *Ds = Qs + C::TILE_BYTES;
+      const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES + w * (C::KC * 8));
+      const int x = (c / C::NCH) / a.grp, ch = c % C::NCH;
+      const int kind = s_kind[x];
+      const float gt = s_gate[x];
+      const int64_t i = s_i[x];
+
+      f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
+      mm_rows_frag<T, D, C::KC / 16>(Qs, kf, sacc, g, p);   // S: query 16m+4g+r, key u
+      mm_rows_frag<T, D, C::KC / 16>(Ds, vf, dpacc, g, p);  // dP
+
+      // valid iff query row (within block i) >= tmin, and the key is in range
+      int tmin = -(1 << 30);
+      bool kok = true;
+      if (kind == KIND_DIAG) tmin = u;
+      else if (kind == KIND_ABS) {
+        const int64_t tm = (int64_t)u - (i - j) * BS;
+        tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);
+        kok = keyok;
+      }
+      tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
+      float pp[C::KC / 16][4], ds[C::KC / 16][4];
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float2 ms = Ms[16 * m + 4 * g + r];
+          const bool ok = kok && (16 * m + r >= tmin);
+          const float pv = ok ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x)) : 0.f;
+          pp[m][r] = pv;
+          ds[m][r] = pv * (dpacc[m][r] - ms.y);
+        }
+      mm_tr_acc<T, D, C::KC>(Ds, pp, dvacc, g, p);  // dV^T += dO^T P
+      mm_tr_acc<T, D, C::KC>(Qs, ds, dkacc, g, p);  // dK^T += Q^T dS
+      lds_barrier();
+    }
+  }
+
+  T *dkrow = (T *)a.dk + ((b * a.Hkv + hk) * a.L + kpos) * D;
+  T *dvrow = (T *)a.dv + ((b * a.Hkv + hk) * a.L + kpos) * D;
+#pragma unroll
+  for (int mt = 0; mt < D / 16; ++mt) {
+    const int d0 = 16 * mt + 4 * g;
+    if constexpr (sizeof(T) == 4) {
+      *(f32x4 *)(dkrow + d0) = f32x4{dkacc[mt][0] * a.scale, dkacc[mt][1] * a.scale, dkacc[mt][2] * a.scale,
+                                     dkacc[mt][3] * a.scale};
+      *(f32x4 *)(dvrow + d0) = dvacc[mt];
+    } else {
+      s16x4 pk, pv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pk[r] = bits16<T>((T)(dkacc[mt][r] * a.scale));
+        pv[r] = bits16<T>((T)dvacc[mt][r]);
+      }
+      *(s16x4 *)(dkrow + d0) = pk;
+      *(s16x4 *)(dvrow + d0) = pv;
+    }
+  }
+}
+
+// dgate[b, hs, i, s] = sum over the heads sharing selection hs (fixed order)
+__global__ __launch_bounds__(256) void dgate_reduce_kernel(const float *part, float *dgate, int64_t n, int64_t Hq,
+                                                           int64_t hsel, int64_t nblk, int64_t kk, int64_t grp) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t s = e % kk, i = (e / kk) % nblk, hs = (e / (kk * nblk)) % hsel, b = e / (kk * nblk * hsel);
+  const int64_t h0 = hsel == 1 ? 0 : hs * grp, nh = hsel == 1 ? Hq : grp;
+  float acc = 0.f;
+  for (int64_t h = h0; h < h0 + nh; ++h) acc += part[((b * Hq + h) * nblk + i) * kk + s];
+  dgate[e] = acc;
+}
+
+static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, BwdArgs &a, const void *dout) {
+  a.B = d->B; a.Hq = d->Hq; a.Hkv = d->Hkv; a.L = d->L; a.nblk = d->nblk; a.kk = d->kk; a.hsel = d->hsel;
+  a.l_valid = d->l_valid;
+  for (int x = 0; x < 3; ++x) { a.sq[x] = d->sq[x]; a.sk[x] = d->sk[x]; a.sv[x] = d->sv[x]; a.sdo[x] = d->sdo[x]; }
+  if (d->flags & FBSA_FLAG_OUT_GATE) {
+    a.dout = ws + lay.dout_attn;
+    a.sdo[0] = d->Hq * d->L * d->D; a.sdo[1] = d->L * d->D; a.sdo[2] = d->D;
+  } else {
+    a.dout = dout;
+  }
+  a.rowstat = (const float2 *)(ws + lay.rowstat);
+  a.seg_off = (const int32_t *)(ws + lay.seg_off);
+  a.ent = (const int32_t *)(ws + lay.vals_out);
+  a.scale = d->scale;
+  a.scale2 = d->scale * kLog2e;
+  a.mask = d->mask;
+  a.grp = (int)(d->Hq / d->Hkv);
+}
+
+template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, const char *what) {
+  if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "%s needs %zu bytes of LDS", what, lds);
+  if (lds > 64 * 1024 && lds > granted) {
+    int e = hip_check(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                      "hipFuncSetAttribute(bwd)");
+    if (e) return e;
+    granted = lds;
+  }
+  return FBSA_OK;
+}
+
+template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipStream_t s) {
+  using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4;
+  static size_t granted = 0;
+  int e = set_lds(dq_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dq");
+  if (e) return e;
+  hipLaunchKernelGGL((dq_kernel<T, BS, D>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
+  return hip_check(hipGetLastError(), "dq_kernel launch");
+}
+
+template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
+  using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 12;
+  static size_t granted = 0;
+  int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
+  if (e) return e;
+  hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)(a.B * a.Hkv * a.nblk)), dim3(C::NT), lds, s, a);
+  return hip_check(hipGetLastError(), "dkdv_kernel launch");
+}
+
+template <typename T, int BS> static int bwd_d(const BwdArgs &a, int64_t D, bool dq, hipStream_t s) {
+  switch (D) {
+    case 32: return dq ? launch_dq<T, BS, 32>(a, s) : launch_dkdv<T, BS, 32>(a, s);
+    case 64: return dq ? launch_dq<T, BS, 64>(a, s) : launch_dkdv<T, BS, 64>(a, s);
+    case 128: return dq ? launch_dq<T, BS, 128>(a, s) : launch_dkdv<T, BS, 128>(a, s);
+    case 256: return dq ? launch_dq<T, BS, 256>(a, s) : launch_dkdv<T, BS, 256>(a, s);
+  }
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: head dim %lld not in {32,64,128,256}", (long long)D);
+}
+
+template <typename T> static int bwd_bs(const BwdArgs &a, int64_t bs, int64_t D, bool dq, hipStream_t s) {
+  switch (bs) {
+    case 16: return bwd_d<T, 16>(a, D, dq, s);
+    case 32: return bwd_d<T, 32>(a, D, dq, s);
+    case 64: return bwd_d<T, 64>(a, D, dq, s);
+    case 128: return bwd_d<T, 128>(a, D, dq, s);
+  }
+  return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: block size %lld not in {16,32,64,128}", (long long)bs);
+}
+
+static int bwd_dispatch(const fbsa_attn_desc *d, const BwdArgs &a, bool dq, hipStream_t s) {
+  switch (d->dtype) {
+    case FBSA_BF16: return bwd_bs<bf16>(a, d->bs, d->D, dq, s);
+    case FBSA_F16: return bwd_bs<f16>(a, d->bs, d->D, dq, s);
+    case FBSA_F32: return bwd_bs<float>(a, d->bs, d->D, dq, s);
+  }
+  return fail(FBSA_EINVAL, "fbsa_bwd: bad dtype %d", d->dtype);
+}
+
+int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
+               const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate, char *ws,
+               hipStream_t s) {
+  BwdArgs a;
+  fill_bwd(d, lay, ws, a, dout);
+  a.q = q; a.k = k; a.v = v; a.sel = sel; a.gate = gate; a.dq = dq; a.dk = a.dv = nullptr;
+  a.dgate_part = dgate ? (float *)(ws + lay.dgate_part) : nullptr;
+  int e = bwd_dispatch(d, a, true, s);
+  if (e || !dgate) return e;
+  const int64_t n = d->B * d->hsel * d->nblk * d->kk;
+  hipLaunchKernelGGL(dgate_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     (const float *)(ws + lay.dgate_part), dgate, n, d->Hq, d->hsel, d->nblk, d->kk,
+                     d->Hq / d->Hkv);
+  return hip_check(hipGetLastError(), "dgate_reduce_kernel launch");
+}
+
+int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
+                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s) {
+  BwdArgs a;
+  fill_bwd(d, lay, ws, a, dout);
+  a.q = q; a.k = k; a.v = v; a.sel = nullptr; a.gate = gate; a.dq = nullptr; a.dk = dk; a.dv = dv;
+  a.dgate_part = nullptr;
+  return bwd_dispatch(d, a, false, s);
+}
+
+}  // namespace fbsa

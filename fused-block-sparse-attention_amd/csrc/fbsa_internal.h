@@ -1,6 +1,7 @@
 // Kernel argument blocks and launch entry points shared by the C ABI layer.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "fbsa.h"
@@ -25,5 +26,25 @@ int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
 int run_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
                float *sel_score, hipStream_t s);
+
+// ---- backward ----
+// Byte offsets of the backward workspace regions (each 256-byte aligned).
+struct BwdLayout {
+  int64_t n;       // sort entries: B * hsel * nblk * kk
+  int64_t nseg;    // CSR segments: B * hsel * nblk
+  int end_bit;     // radix-sort key bits
+  size_t rowstat, dout_attn, dgate_part, keys_in, keys_out, vals_in, vals_out, seg_off, sort_tmp;
+  size_t sort_tmp_bytes, total;
+};
+
+int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay);
+int run_bwd_prep(const fbsa_attn_desc *d, const BwdLayout &lay, const void *o, const void *dout, const float *lse,
+                 const void *out_gate, void *dout_gate, char *ws, hipStream_t s);
+int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int32_t *sel, char *ws, hipStream_t s);
+int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
+               const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate, char *ws,
+               hipStream_t s);
+int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
+                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s);
 
 }  // namespace fbsa

@@ -1,0 +1,162 @@
+// Tile-level building blocks shared by the backward kernels (gfx950).
+//
+// A "tile" is ROWS x D elements in LDS, each row CPR = D*sizeof(T)/16 chunks
+// of 16 bytes, logical chunk c of row r stored at position c ^ swz(r, CPR).
+// Lanes are (g, p) = (lane / 16, lane % 16). Two products cover every
+// contraction of the attention backward:
+//
+//   mm_rows_frag : acc[m][r]  = sum_d tile[16m + 4g + r][d] * frag_p[d]
+//                  (tile rows as the MFMA A operand, one 16-row register
+//                  fragment as B: S = Q K^T, dP = dO V^T and transposes)
+//   mm_tr_acc    : acc[t][r] += sum_k tile[k][16t + 4g + r] * x_p[k]
+//                  (tile^T as A through transposing LDS reads, x given as
+//                  per-lane values x[m][r] at k = 16m + 4g + r: dQ = dS K,
+//                  dK = dS^T Q, dV = P^T dO)
+#pragma once
+#include "fbsa_common.h"
+
+namespace fbsa {
+
+// Row fragment: lane (g, p) holds row p's elements k = 32ks + 8g + e (16-bit
+// types) or k = 4ks + g (fp32).
+template <typename T, int D> struct RowFrag {
+  static constexpr bool F32 = sizeof(T) == 4;
+  static constexpr int N = F32 ? D / 4 : D / 32;
+  s16x8 h[F32 ? 1 : N];
+  float f[F32 ? N : 1];
+  __device__ __forceinline__ void load(const T *row, int g) {
+    if constexpr (F32) {
+#pragma unroll
+      for (int ks = 0; ks < N; ++ks) f[ks] = ((const float *)row)[4 * ks + g];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < N; ++ks) h[ks] = *(const s16x8 *)(row + 32 * ks + 8 * g);
+    }
+  }
+};
+
+template <typename T, int D, int NM>
+__device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p) {
+  constexpr int CPR = D * (int)sizeof(T) / 16;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * m + p;
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int ks = 0; ks < D / 4; ++ks) {
+        const float x = *(const float *)(tile + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
+        acc[m] = mfma_f32_16x16x4(x, fr.f[ks], acc[m]);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) {
+        const s16x8 x = *(const s16x8 *)(tile + (row * CPR + ((4 * ks + g) ^ swz(row, CPR))) * 16);
+        acc[m] = Mfma16<T>::run(x, fr.h[ks], acc[m]);
+      }
+    }
+  }
+}
+
+template <typename T, int D, int KC>
+__device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC / 16][4], f32x4 *acc, int g, int p) {
+  constexpr int CPR = D * (int)sizeof(T) / 16;
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int m = 0; m < KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * m + 4 * g + r;
+          const float a = *(const float *)(tile + (row * CPR + ((4 * t + (p >> 2)) ^ swz(row, CPR))) * 16 + (p & 3) * 4);
+          acc[t] = mfma_f32_16x16x4(a, x[m][r], acc[t]);
+        }
+  } else if constexpr (KC >= 32) {
+    s16x8 pk[KC / 32];
+#pragma unroll
+    for (int k2 = 0; k2 < KC / 32; ++k2) {
+      float y[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { y[r] = x[2 * k2][r]; y[4 + r] = x[2 * k2 + 1][r]; }
+      pk[k2] = pack8<T>(y);
+    }
+    s16x4 lo[D / 16][KC / 32], hi[D / 16][KC / 32];
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const int cb = 2 * t + ((p & 3) >> 1);
+#pragma unroll
+      for (int k2 = 0; k2 < KC / 32; ++k2) {
+        const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
+        lo[t][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
+        hi[t][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
+      }
+    }
+    lds_wait_all();
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int k2 = 0; k2 < KC / 32; ++k2) {
+        lds_ready(lo[t][k2]);
+        lds_ready(hi[t][k2]);
+        const s16x4 a = lo[t][k2], b = hi[t][k2];
+        const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        acc[t] = Mfma16<T>::run(av, pk[k2], acc[t]);
+      }
+  } else {
+    s16x4 pk;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)x[0][r]);
+    s16x4 a[D / 16];
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const int cb = 2 * t + ((p & 3) >> 1);
+      const int ra = 4 * g + (p >> 2);
+      a[t] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
+    }
+    lds_wait_all();
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      lds_ready(a[t]);
+      acc[t] = Mfma16<T>::run16(a[t], pk, acc[t]);
+    }
+  }
+}
+
+// Copy KC rows from each of two row-major sources into one LDS stage (two
+// swizzled tiles back to back) with direct-to-LDS 16-byte loads; every thread
+// issues LPT loads. Rows are src + (row0 + r) * stride.
+template <typename T, int KC, int D, int NW, int LPT>
+__device__ __forceinline__ void issue_tile_pair(char *st, const T *src0, int64_t stride0, const T *src1,
+                                                int64_t stride1, int64_t row0, int w, int lane) {
+  constexpr int CPR = D * (int)sizeof(T) / 16;
+  constexpr int ES = (int)sizeof(T);
+#pragma unroll
+  for (int n = 0; n < LPT; ++n) {
+    const int wl = n * NW + w;
+    const int u = wl * 64 + lane;
+    const int part = u / (KC * CPR);
+    const int rem = u - part * (KC * CPR);
+    const int row = rem / CPR, pos = rem % CPR;
+    const int chunk = pos ^ swz(row, CPR);
+    const T *src = part ? src1 + (row0 + row) * stride1 : src0 + (row0 + row) * stride0;
+    g2lds16(src + chunk * (16 / ES), st + wl * 1024);
+  }
+}
+
+}  // namespace fbsa
+
+namespace fbsa {
+
+// Wait until at most `pending` ring stages of N direct-to-LDS loads each are
+// still in flight (the loads of older stages have landed).
+template <int N> __device__ __forceinline__ void wait_ring(int pending) {
+  switch (pending) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<(N < 64 ? N : 63)>(); break;
+    case 2: wait_vmcnt<(2 * N < 64 ? 2 * N : 63)>(); break;
+    default: wait_vmcnt<(3 * N < 64 ? 3 * N : 63)>(); break;
+  }
+}
+
+}  // namespace fbsa

@@ -16,6 +16,7 @@ OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 POOL_MEAN_TOK_THEN_GRP, POOL_MEAN_GRP_THEN_TOK, POOL_MAX, POOL_MIN, POOL_MINMAX = 0, 1, 2, 3, 4
 SCORE_DOT, SCORE_MAX2, SCORE_QUEST = 0, 1, 2
 SEL_OWN_FIRST, SEL_SORTED_SINK = 0, 1
+FLAG_OUT_GATE = 1
 
 _i64x3 = ctypes.c_int64 * 3
 
@@ -65,11 +66,11 @@ SIGNATURES = {
     "fbsa_select_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SelectDesc)]),
     "fbsa_select": (ctypes.c_int, [ctypes.POINTER(SelectDesc), _vp, _vp, _vp, _vp, _vp, _vp,
                                    ctypes.c_size_t, _vp]),
-    "fbsa_bwd_prep": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp]),
     "fbsa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnDesc)]),
+    "fbsa_bwd_prep": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 6 + [ctypes.c_size_t, _vp]),
     "fbsa_transpose_index": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, ctypes.c_size_t, _vp]),
-    "fbsa_bwd_dq": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 14),
-    "fbsa_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 10 + [ctypes.c_size_t, _vp, _vp, _vp]),
+    "fbsa_bwd_dq": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 9 + [ctypes.c_size_t, _vp]),
+    "fbsa_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 8 + [ctypes.c_size_t, _vp]),
     "fbsa_bwd": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 15 + [ctypes.c_size_t, _vp]),
 }
 

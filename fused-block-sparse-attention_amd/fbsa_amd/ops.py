@@ -131,3 +131,63 @@ def attention_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None
     if Dp != D:
         o = o[..., :D]
     return (o, lse) if need_lse else o
+
+
+def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=None, l_valid=None,
+                       out_gate=None, need_dgate=False):
+    """Backward of ``attention_forward`` (no atomics; bitwise repeatable).
+
+    o and lse are the forward's outputs (o gated when out_gate is given).
+    Returns (dq, dk, dv, dgate, dout_gate): dq (B,Hq,L,D), dk/dv (B,Hkv,L,D) in
+    q's dtype; dgate (B,Hsel,nblk,kk) fp32 when need_dgate (the gradient of the
+    additive gate, summed over the heads sharing the selection), else None;
+    dout_gate (B,Hq,L,D) when out_gate is given, else None.
+    """
+    _check_common(q, k, v, sel, gate)
+    _require_cuda(o, lse, dout, out_gate)
+    B, Hq, L, D = q.shape
+    if o.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("fbsa: o and dout must have q's shape")
+    if lse.shape != (B, Hq, L) or lse.dtype != torch.float32:
+        raise ValueError("fbsa: lse must be fp32 (B, Hq, L)")
+    scale = D ** -0.5 if scale is None else scale
+    Dp = padded_head_dim(D)
+    qk = [_kernel_ready(_pad_d(t, Dp)) for t in (q, k, v)]
+    o_p = _kernel_ready(_pad_d(o.to(q.dtype), Dp))
+    do_p = _kernel_ready(_pad_d(dout.to(q.dtype), Dp))
+    og = None
+    if out_gate is not None:
+        if out_gate.shape != q.shape or out_gate.dtype != q.dtype:
+            raise ValueError("fbsa: out_gate must match q's shape and dtype")
+        og = _pad_d(out_gate, Dp)
+        if og.stride(-1) != 1:
+            og = og.contiguous()
+    sel32 = sel.to(torch.int32).contiguous()
+    gate32 = gate.to(torch.float32).contiguous() if gate is not None else None
+    lse_c = lse.contiguous()
+    nblk = sel32.shape[2]
+    if nblk == 0 or L % nblk:
+        raise ValueError(f"fbsa: L={L} is not a multiple of nblk={nblk}")
+    dev = q.device
+    dq = torch.empty(B, Hq, L, Dp, dtype=q.dtype, device=dev)
+    dk = torch.empty(B, k.shape[1], L, Dp, dtype=q.dtype, device=dev)
+    dv = torch.empty_like(dk)
+    dgate = torch.empty(sel32.shape, dtype=torch.float32, device=dev) if need_dgate else None
+    dog = torch.empty(B, Hq, L, Dp, dtype=q.dtype, device=dev) if og is not None else None
+    d = make_desc(qk[0], qk[1], qk[2], o_p, sel32, mask=mask, scale=scale, l_valid=l_valid, dout=do_p,
+                  out_gate=og)
+    d.flags = _lib.FLAG_OUT_GATE if og is not None else 0
+    lib = _lib.load()
+    nbytes = lib.fbsa_bwd_workspace_bytes(d)
+    if nbytes == 0:
+        _lib.check(_lib.EINVAL, "fbsa_bwd_workspace_bytes")
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=dev)
+    base = ws.data_ptr()
+    wp = (base + 255) // 256 * 256
+    _lib.check(lib.fbsa_bwd(d, _ptr(qk[0]), _ptr(qk[1]), _ptr(qk[2]), _ptr(o_p), _ptr(do_p), _ptr(lse_c),
+                            _ptr(sel32), _ptr(gate32), _ptr(og), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dgate),
+                            _ptr(dog), wp, nbytes, _stream()), "fbsa_bwd")
+    if Dp != D:
+        dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+        dog = dog[..., :D] if dog is not None else None
+    return dq, dk, dv, dgate, dog

@@ -57,7 +57,7 @@ typedef struct fbsa_attn_desc {
   int64_t hsel;    /* 1 or Hkv */
   int64_t l_valid; /* positions >= l_valid are padding keys (TOKEN_CAUSAL) */
   float scale;     /* softmax scale applied to q.k before the gate bias */
-  int32_t flags;   /* reserved, 0 */
+  int32_t flags;   /* FBSA_FLAG_* bits (backward only; 0 for the forward) */
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sog[3];
 } fbsa_attn_desc;
 
@@ -129,38 +129,56 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
 
 /* ---- backward -------------------------------------------------------- */
 
-/* delta[b,h,t] = sum_d do*o (o as written by fbsa_fwd, gated or not). */
-int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, float *delta,
+/* fbsa_attn_desc.flags bits. OUT_GATE: the backward will be given out_gate
+ * (the forward applied o <- o * sigmoid(out_gate)); the workspace then also
+ * holds the gate-scaled upstream gradient. */
+enum { FBSA_FLAG_OUT_GATE = 1 };
+
+/* Workspace for the backward stages below (one opaque region, 256-byte
+ * aligned): per-row softmax statistics, the block-transposed index (CSR of
+ * the valid (query block, slot) pairs per key block, sorted by a stable radix
+ * sort so the dK/dV summation order is fixed), per-head gate-gradient
+ * partials and, with FBSA_FLAG_OUT_GATE, the gate-scaled dO.
+ * Returns 0 (with fbsa_last_error set) when the descriptor is invalid. */
+size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *d);
+
+/* Stage 1. Row statistics: delta[b,h,t] = sum_d dout*o and lse*log2(e) into
+ * the workspace. With out_gate (FBSA_FLAG_OUT_GATE): dout_gate = dout*o*
+ * (1 - sigmoid(out_gate)) (B,Hq,L,D contiguous) and the workspace copy
+ * dout*sigmoid(out_gate) used by the later stages. o, dout strides: so, sdo. */
+int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, const float *lse,
+                  const void *out_gate, void *dout_gate, void *workspace, size_t workspace_bytes,
                   void *stream);
 
-/* Block-transposed index: for each (b, hsel, key block j) the (i, slot)
- * pairs that attend to it, in ascending (i, slot) order (deterministic CSR).
- * Uses the workspace; must precede fbsa_bwd_dkdv. */
-size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *d);
+/* Stage 2. Block-transposed index of sel: for each (b, hsel, key block j) the
+ * valid (i, slot) pairs that read it, ascending (deterministic CSR). */
 int fbsa_transpose_index(const fbsa_attn_desc *d, const int32_t *sel, void *workspace,
                          size_t workspace_bytes, void *stream);
 
-/* dq (B,Hq,L,D contiguous) and, when dgate != NULL, the fp32 gate gradient
- * (B,Hsel,nblk,kk); when out_gate != NULL also dout_gate (strides sog). */
+/* Stage 3. dq (B,Hq,L,D contiguous) over each query block's selected key
+ * blocks; when dgate != NULL also the fp32 gate gradient (B,Hsel,nblk,kk),
+ * summed over the heads sharing a selection in a fixed order (0 for masked
+ * slots). Needs stage 1. */
 int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
-                const void *o, const void *dout, const float *lse, const float *delta,
-                const int32_t *sel, const float *gate, const void *out_gate,
-                void *dq, float *dgate, void *dout_gate, void *stream);
+                const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate,
+                void *workspace, size_t workspace_bytes, void *stream);
 
-/* dk, dv (B,Hkv,L,D contiguous), atomics-free over the transposed index. */
+/* Stage 4. dk, dv (B,Hkv,L,D contiguous), one workgroup per key block walking
+ * its transposed list (and the GQA group's query heads) in order: no atomics,
+ * bitwise repeatable. Needs stages 1 and 2. */
 int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
-                  const void *dout, const float *lse, const float *delta,
-                  const int32_t *sel, const float *gate, const void *out_gate,
-                  const void *workspace, size_t workspace_bytes,
-                  void *dk, void *dv, void *stream);
+                  const void *dout, const float *gate, void *dk, void *dv, void *workspace,
+                  size_t workspace_bytes, void *stream);
 
-/* All of the above in order. Replaces _bsattn_bwd / bsattn_backward
- * (src/triton_kernel.py:77-181, 210-234). */
-int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
-             const void *o, const void *dout, const float *lse, const int32_t *sel,
-             const float *gate, const void *out_gate, void *dq, void *dk, void *dv,
-             float *dgate, void *dout_gate, void *workspace, size_t workspace_bytes,
-             void *stream);
+/* All four stages in order. lse is the forward's (fbsa_fwd) output; o is the
+ * forward output (gated when out_gate != NULL). dgate and dout_gate are
+ * nullable. Replaces _bsattn_bwd / bsattn_backward
+ * (src/triton_kernel.py:77-181, 210-234) and the autograd of the gather path
+ * (src/ssa_model.py:57-90). */
+int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o,
+             const void *dout, const float *lse, const int32_t *sel, const float *gate,
+             const void *out_gate, void *dq, void *dk, void *dv, float *dgate, void *dout_gate,
+             void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -123,7 +123,7 @@ def fwd(q, k, v, sel, mask, scale=None, gate=None, L_valid=None, out_gate=None, 
     return o, lse
 
 
-def bwd(q, k, v, sel, do, mask, scale=None, gate=None, L_valid=None, out_gate=None):
+def bwd(q, k, v, sel, do, mask, scale=None, gate=None, L_valid=None, out_gate=None, rows=None):
     """Backward of ``fwd`` by explicit softmax calculus (float64).
 
     Returns dq, dk, dv (shapes of q, k, v), dgate (B,Hs,nblk,kk) and dout_gate
@@ -132,7 +132,12 @@ def bwd(q, k, v, sel, do, mask, scale=None, gate=None, L_valid=None, out_gate=No
     which is what the reference's atomics compute (``src/triton_kernel.py:178-179``).
     dgate sums the score gradient over the slot's keys, the block's queries and
     the heads sharing the selection (the gradient the gather path gives the
-    gate, ``src/ssa_model.py:72-74``; the fused reference op returns None)."""
+    gate, ``src/ssa_model.py:72-74``; the fused reference op returns None).
+
+    ``rows`` restricts the computation to the contributions of those query
+    blocks (dq and dgate of other rows stay 0; dk/dv hold only those rows'
+    contributions -- complete for a key block when ``rows`` covers every row
+    that selected it)."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
@@ -145,16 +150,21 @@ def bwd(q, k, v, sel, do, mask, scale=None, gate=None, L_valid=None, out_gate=No
     grp, hsel = _head_maps(Hq, Hkv, Hs)
     scale = D ** -0.5 if scale is None else scale
     L_valid = N if L_valid is None else L_valid
-    o, lse = fwd(q, k, v, sel, mask, scale, gate, L_valid, None)
+    rows = np.arange(nblk) if rows is None else np.asarray(rows, dtype=np.int64)
+    o_r, lse_r = fwd(q, k, v, sel, mask, scale, gate, L_valid, None, rows=rows)   # (B,Hq,R*bs,*)
+    R = len(rows)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
     dv = np.zeros_like(v)
     dgate = np.zeros(sel.shape)
     dog = None
+    do_r = do.reshape(B, Hq, nblk, bs, D)[:, :, rows]                              # (B,Hq,R,bs,D)
     if out_gate is not None:
-        sg = _sigmoid(np.asarray(out_gate, dtype=np.float64))
-        dog = do * o * sg * (1.0 - sg)
-        do = do * sg
+        og_r = np.asarray(out_gate, dtype=np.float64).reshape(B, Hq, nblk, bs, D)[:, :, rows]
+        sg = _sigmoid(og_r)
+        dog = np.zeros_like(q)
+        dog.reshape(B, Hq, nblk, bs, D)[:, :, rows] = do_r * o_r.reshape(B, Hq, R, bs, D) * sg * (1.0 - sg)
+        do_r = do_r * sg
     for b in range(B):
         for hq in range(Hq):
             hk = hq // grp
@@ -162,31 +172,32 @@ def bwd(q, k, v, sel, do, mask, scale=None, gate=None, L_valid=None, out_gate=No
             kb = k[b, hk].reshape(nblk, bs, D)
             vb = v[b, hk].reshape(nblk, bs, D)
             qb = q[b, hq].reshape(nblk, bs, D)
-            dob = do[b, hq].reshape(nblk, bs, D)
-            ob = o[b, hq].reshape(nblk, bs, D)
-            lseb = lse[b, hq].reshape(nblk, bs)
+            dqb = dq[b, hq].reshape(nblk, bs, D)
             dkb = dk[b, hk].reshape(nblk, bs, D)
             dvb = dv[b, hk].reshape(nblk, bs, D)
-            for r0, r1 in _chunks(nblk, bs, kk, D):
-                rr = np.arange(r0, r1)
+            ob = o_r[b, hq].reshape(R, bs, D)
+            lseb = lse_r[b, hq].reshape(R, bs)
+            for r0, r1 in _chunks(R, bs, kk, D):
+                rr = rows[r0:r1]
                 s_rows = sel[b, hs, rr]
                 kg, vg = kb[s_rows], vb[s_rows]
                 lg = np.einsum("rtd,rsud->rtsu", qb[rr], kg) * scale
                 if gate is not None:
                     lg = lg + np.asarray(gate, dtype=np.float64)[b, hs, rr][:, None, :, None]
                 ok = _valid(s_rows, rr, bs, mask, L_valid)
-                ls = lseb[rr]
+                ls = lseb[r0:r1]
                 ls_safe = np.where(np.isfinite(ls), ls, 0.0)
                 p = np.where(ok, np.exp(np.where(ok, lg, 0.0) - ls_safe[:, :, None, None]), 0.0)
                 p = np.where(np.isfinite(ls)[:, :, None, None], p, 0.0)
-                Dr = (dob[rr] * ob[rr]).sum(-1)                                  # (r, t)
-                dp = np.einsum("rtd,rsud->rtsu", dob[rr], vg)
+                dor = do_r[b, hq, r0:r1]
+                Dr = (dor * ob[r0:r1]).sum(-1)                                   # (r, t)
+                dp = np.einsum("rtd,rsud->rtsu", dor, vg)
                 ds = p * (dp - Dr[:, :, None, None])
-                dq[b, hq].reshape(nblk, bs, D)[rr] += scale * np.einsum("rtsu,rsud->rtd", ds, kg)
+                dqb[rr] += scale * np.einsum("rtsu,rsud->rtd", ds, kg)
                 np.add.at(dkb, s_rows.reshape(-1),
                           (scale * np.einsum("rtsu,rtd->rsud", ds, qb[rr])).reshape(-1, bs, D))
                 np.add.at(dvb, s_rows.reshape(-1),
-                          np.einsum("rtsu,rtd->rsud", p, dob[rr]).reshape(-1, bs, D))
+                          np.einsum("rtsu,rtd->rsud", p, dor).reshape(-1, bs, D))
                 dgate[b, hs, rr] += ds.sum(axis=(1, 3))
     return dq, dk, dv, dgate, dog
 
