@@ -35,7 +35,7 @@
 
 namespace fbsa {
 
-enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2 };
+enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 
 #ifndef FBSA_DQ_LDS_BUDGET
 #define FBSA_DQ_LDS_BUDGET 32768
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void keys_kernel(IdxArgs a) {
   const int64_t j = row[s];
   const bool inb = j >= 0 && j < a.nblk;
   bool valid;
-  if (a.mask == FBSA_MASK_NONE) valid = inb;
+  if (a.mask == FBSA_MASK_NONE) valid = inb && j * a.bs < a.l_valid;
   else if (a.mask == FBSA_MASK_SLOT_CAUSAL) valid = s == 0 ? inb : (inb && j < i);
   else {
     valid = inb && j <= i && j * a.bs < a.l_valid;
@@ -315,7 +315,8 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
         j = selrow[s];
         const bool inb = j >= 0 && j < a.nblk;
         if (a.mask == FBSA_MASK_NONE) {
-          valid = inb;
+          valid = inb && (int64_t)j * BS < a.l_valid;
+          if (valid && (int64_t)(j + 1) * BS > a.l_valid) kind = KIND_PAD;
         } else if (a.mask == FBSA_MASK_SLOT_CAUSAL) {
           if (s == 0) { valid = inb; kind = KIND_DIAG; }
           else valid = inb && j < i;
@@ -388,8 +389,9 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     int lim = 1 << 30;
     if (kind != KIND_FULL) {
       const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
-                                              : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
-                                                                                            : a.l_valid - j * BS - 1);
+                            : kind == KIND_PAD  ? a.l_valid - j * BS - 1
+                                                : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
+                                                                                              : a.l_valid - j * BS - 1);
       lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
     }
     const float off = gt - lse2;
@@ -481,6 +483,7 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
       const int i = (int)(ev / a.kk), s = (int)(ev % a.kk);
       int kind = KIND_FULL;
       if (a.mask == FBSA_MASK_SLOT_CAUSAL) kind = s == 0 ? KIND_DIAG : KIND_FULL;
+      else if (a.mask == FBSA_MASK_NONE) kind = (j + 1) * BS > a.l_valid ? KIND_PAD : KIND_FULL;
       else if (a.mask == FBSA_MASK_TOKEN_CAUSAL)
         kind = (j == i || (j + 1) * BS > a.l_valid) ? KIND_ABS : KIND_FULL;
       s_i[x] = i;
@@ -526,6 +529,7 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
       int tmin = -(1 << 30);
       bool kok = true;
       if (kind == KIND_DIAG) tmin = u;
+      else if (kind == KIND_PAD) kok = keyok;
       else if (kind == KIND_ABS) {
         const int64_t tm = (int64_t)u - (i - j) * BS;
         tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);

@@ -19,7 +19,7 @@
 
 namespace fbsa {
 
-enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2 };
+enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 
 // LDS bytes per workgroup for the K/V prefetch ring (sets the ring depth).
 #ifndef FBSA_FWD_LDS_BUDGET
@@ -86,7 +86,8 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
         j = selrow[s];
         const bool inb = j >= 0 && j < a.nblk;
         if (a.mask == FBSA_MASK_NONE) {
-          valid = inb;
+          valid = inb && (int64_t)j * BS < a.l_valid;
+          if (valid && (int64_t)(j + 1) * BS > a.l_valid) kind = KIND_PAD;
         } else if (a.mask == FBSA_MASK_SLOT_CAUSAL) {
           if (s == 0) { valid = inb; kind = KIND_DIAG; }
           else valid = inb && j < i;
@@ -191,8 +192,9 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
     // skips the compares for unmasked chunks, the common case)
     if (kind != KIND_FULL) {
       const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
-                                              : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
-                                                                                            : a.l_valid - j * BS - 1);
+                            : kind == KIND_PAD  ? a.l_valid - j * BS - 1
+                                                : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
+                                                                                              : a.l_valid - j * BS - 1);
       const int lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;  // compare against 16m + r
 #pragma unroll
       for (int m = 0; m < C::KC / 16; ++m)

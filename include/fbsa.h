@@ -36,7 +36,9 @@ extern "C" {
 enum { FBSA_F32 = 0, FBSA_BF16 = 1, FBSA_F16 = 2 };
 
 /* Attention mask rules.
- * NONE         every key of every slot (src/triton_kernel.py:20-74 with CAUSAL=False)
+ * NONE         every key of every slot at a position < l_valid
+ *              (src/triton_kernel.py:20-74 with CAUSAL=False; l_valid < L only
+ *              for the padded non-causal dense path, src/qwen_blocksparse.py:37-41)
  * SLOT_CAUSAL  slot 0: key row <= query row; slot s>0 valid iff sel < i
  *              (src/triton_kernel.py:57-61; src/ssa_model.py:167-183)
  * TOKEN_CAUSAL key pos <= query pos, key pos < l_valid, first occurrence of the
@@ -55,7 +57,7 @@ typedef struct fbsa_attn_desc {
   int64_t bs;      /* block size: 16, 32, 64 or 128 */
   int64_t nblk, kk;
   int64_t hsel;    /* 1 or Hkv */
-  int64_t l_valid; /* positions >= l_valid are padding keys (TOKEN_CAUSAL) */
+  int64_t l_valid; /* positions >= l_valid are padding keys (NONE, TOKEN_CAUSAL) */
   float scale;     /* softmax scale applied to q.k before the gate bias */
   int32_t flags;   /* FBSA_FLAG_* bits (backward only; 0 for the forward) */
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sog[3];

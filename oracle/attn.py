@@ -9,8 +9,10 @@ softmax scale (``src/triton_kernel.py:62-64``; ``src/ssa_model.py:71-74``).
 
 Mask rules (``mask``):
 
-* ``"none"``        -- every key of every slot (non-causal BlockSparseSSA and
-                       ``bsattn(causal=False)``; duplicates count twice).
+* ``"none"``        -- every key of every slot at a position < L_valid
+                       (non-causal BlockSparseSSA and ``bsattn(causal=False)``;
+                       duplicates count twice; L_valid < N only for the padded
+                       non-causal dense path, ``src/qwen_blocksparse.py:37-41``).
 * ``"slot_causal"`` -- slot 0: key row u <= query row t (triu on the own
                        block); slot s>0: whole slot valid iff sel < i.
                        ``src/triton_kernel.py:57-61``; ``src/ssa_model.py:167-183``.
@@ -32,7 +34,8 @@ def _valid(sel_rows, rows, bs, mask, L_valid):
     R, kk = sel_rows.shape
     t = np.arange(bs)
     if mask == "none":
-        return np.ones((R, bs, kk, bs), dtype=bool)
+        keypos = sel_rows[:, :, None] * bs + t[None, None, :]      # (R, kk, bs)
+        return np.broadcast_to((keypos < L_valid)[:, None, :, :], (R, bs, kk, bs)).copy()
     if mask == "slot_causal":
         v = np.ones((R, bs, kk, bs), dtype=bool)
         v[:, :, 0, :] = t[None, None, :] <= t[None, :, None]      # u <= t on slot 0
@@ -234,7 +237,7 @@ def fwd_bruteforce(q, k, v, sel, mask, scale=None, gate=None, L_valid=None):
                         elif mask == "token_causal":
                             ok = kpos <= pos and kpos < L_valid and j not in row[:s]
                         else:
-                            ok = True
+                            ok = kpos < L_valid
                         if not ok:
                             continue
                         g = 0.0 if gate is None else float(gate[b, hs, i, s])

@@ -1,0 +1,253 @@
+"""GPU tests of the reference-compatible surfaces: ``triton_kernel``,
+``ssa_model.BlockSparseSSA`` and ``qwen_blocksparse`` (drop-ins for the
+reference's modules of the same names), against the CPU oracle and the
+reference's own closed-form checks."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attn as oattn, select as osel
+from _util import randn, np64, assert_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(*a):
+    print("[surface]", *a, flush=True)
+
+
+# ---------------------------------------------------------------- triton_kernel
+def test_triton_kernel_forward_backward_match_oracle():
+    import triton_kernel as tk
+    g = torch.Generator().manual_seed(0)
+    B, H, N, D, bs, kk = 2, 2, 512, 64, 32, 5
+    nblk = N // bs
+    q, k, v, do = (randn(g, (B, H, N, D), "bf16") for _ in range(4))
+    rnd = torch.randint(0, nblk, (B, nblk, kk - 1), generator=g)
+    sel = torch.cat([torch.arange(nblk).view(1, nblk, 1).expand(B, nblk, 1), rnd], -1)
+    gate = F.logsigmoid(torch.randn(B, nblk, kk, generator=g))
+    for causal in (False, True):
+        _say("bsattn_forward/backward causal", causal)
+        mask = "slot_causal" if causal else "none"
+        o = tk.bsattn_forward(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV), gate.to(DEV), causal=causal)
+        ro, _ = oattn.fwd(np64(q), np64(k), np64(v), sel.numpy()[:, None], mask, gate=gate.numpy()[:, None])
+        assert o.dtype == q.dtype and o.shape == q.shape
+        assert_close(np64(o), ro, "bf16", "o")
+        dq, dk, dv = tk.bsattn_backward(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV), o, do.to(DEV),
+                                        gate.to(DEV), causal=causal)
+        r = oattn.bwd(np64(q), np64(k), np64(v), sel.numpy()[:, None], np64(do), mask, gate=gate.numpy()[:, None])
+        for n, a, b in (("dq", dq, r[0]), ("dk", dk, r[1]), ("dv", dv, r[2])):
+            assert_close(np64(a), b, "bf16", n)
+
+
+def test_triton_kernel_rejects_bad_length():
+    import triton_kernel as tk
+    q = torch.zeros(1, 1, 100, 64, dtype=torch.bfloat16, device=DEV)
+    sel = torch.zeros(1, 3, 1, dtype=torch.int32, device=DEV)
+    with pytest.raises(AssertionError):
+        tk.bsattn_forward(q, q, q, sel)
+
+
+# ---------------------------------------------------------------- ssa_model
+def test_blocksparse_all_blocks_equals_dense_gate():
+    # the reference's correctness gate (scripts/run_all.sh:7-21), on the GPU
+    from ssa_model import BlockSparseSSA, DenseAttention
+    torch.manual_seed(0)
+    B, L, D, H = 2, 512, 128, 4
+    x = torch.randn(B, L, D, device=DEV)
+    sp = BlockSparseSSA(D, H, block=64, topk=10_000, sel_dim=16).to(DEV)
+    dn = DenseAttention(D, H).to(DEV)
+    dn.qkv.load_state_dict(sp.qkv.state_dict())
+    dn.o.load_state_dict(sp.o.state_dict())
+    with torch.no_grad():
+        diff = (dn(x) - sp(x)).abs().max().item()
+    _say("max|dense - sparse(all blocks)| =", diff)
+    assert diff < 1e-3
+    # causal, topk >= nblk-1 (every past block) == causal dense
+    sp.causal, dn.causal = True, True
+    with torch.no_grad():
+        diff = (dn(x) - sp(x)).abs().max().item()
+    _say("causal: max|dense - sparse(all blocks)| =", diff)
+    assert diff < 1e-3
+    # more blocks than the streaming top-k holds: own + every other block
+    sp = BlockSparseSSA(D, H, block=16, topk=10_000, sel_dim=16, causal=True, gate=False).to(DEV)
+    dn = DenseAttention(D, H, causal=True).to(DEV)
+    dn.qkv.load_state_dict(sp.qkv.state_dict())
+    dn.o.load_state_dict(sp.o.state_dict())
+    x = torch.randn(1, 16 * 80, D, device=DEV)
+    with torch.no_grad():
+        diff = (dn(x) - sp(x)).abs().max().item()
+    _say("nblk=80 causal: max|dense - sparse(all blocks)| =", diff)
+    assert diff < 1e-3
+
+
+def _module_oracle(m, x):
+    """The reference module's computation restated on the oracle: q,k,v and the
+    pooled selector features come from the module's own layers (torch, GPU);
+    selection, gate and attention from the oracle; output projection in fp64."""
+    B, L, D = x.shape
+    Bs, H, dh = m.block, m.h, m.dh
+    nblk = L // Bs
+    dt = osel.__dict__  # noqa: F841
+    name = {torch.float32: "f32", torch.bfloat16: "bf16"}[x.dtype]
+    with torch.no_grad():
+        q, k, v = (t.view(B, L, H, dh).transpose(1, 2) for t in m.qkv(x).chunk(3, -1))
+        sq, skm, skx = m._pooled(x, B, nblk, Bs)
+    raw = osel.scores(np64(sq), np64(skm), name, "max2", b2=np64(skx))
+    sel = osel.select_conv_a(raw, m.topk, m.causal)
+    gate = None
+    if m.gate:
+        from oracle.numerics import round_to
+        gate = round_to(osel.gate_from_scores(raw, sel), name)[:, None]
+    o, _ = oattn.fwd(np64(q), np64(k), np64(v), sel[:, None], "slot_causal" if m.causal else "none", gate=gate)
+    o = o.transpose(0, 2, 1, 3).reshape(B, L, D)
+    W, b = np64(m.o.weight), np64(m.o.bias)
+    return o @ W.T + b, sel
+
+
+@pytest.mark.parametrize("causal,gate", [(True, True), (False, False), (True, False)])
+def test_blocksparse_module_matches_oracle(causal, gate):
+    # verify_kernel.py's "small" case shape: d256 h4 B2 L1024 block64 top-4, bf16
+    from ssa_model import BlockSparseSSA
+    torch.manual_seed(0)
+    m = BlockSparseSSA(256, 4, block=64, topk=4, causal=causal, gate=gate).to(DEV).to(torch.bfloat16).eval()
+    x = torch.randn(2, 1024, 256, device=DEV, dtype=torch.bfloat16)
+    _say("module", causal, gate)
+    with torch.no_grad():
+        m.use_triton = False
+        a = m(x)
+        m.use_triton = True
+        b = m(x)
+    assert torch.equal(a, b)
+    ref, _ = _module_oracle(m, x)
+    assert_close(np64(a), ref, "bf16", "module out")
+
+
+def test_blocksparse_gate_gradient_paths():
+    # gather path (use_triton=False) trains the selector through the gate; the
+    # fused op (use_triton=True) returns no gate gradient (src/triton_kernel.py:254)
+    from ssa_model import BlockSparseSSA
+    torch.manual_seed(1)
+    m = BlockSparseSSA(128, 2, block=32, topk=3, causal=True, gate=True).to(DEV)
+    x = torch.randn(2, 512, 128, device=DEV, requires_grad=True)
+    m.use_triton = False
+    m(x).square().sum().backward()
+    gq = m.sel_q[0].weight.grad
+    assert gq is not None and gq.abs().sum() > 0 and m.qkv.weight.grad.abs().sum() > 0
+    m.zero_grad(set_to_none=True)
+    m.use_triton = True
+    m(x).square().sum().backward()
+    assert m.sel_q[0].weight.grad is None and m.qkv.weight.grad.abs().sum() > 0
+
+
+def test_blocksparse_gate_gradient_matches_finite_difference():
+    # d(loss)/d(selector params) through logsigmoid(raw[i, sel]) on the fused backward, fp32
+    from ssa_model import BlockSparseSSA
+    torch.manual_seed(2)
+    # a bias on the key-side selector output shifts every block's pooled mean
+    # and max alike, so the selected blocks do not change under the perturbation
+    m = BlockSparseSSA(64, 2, block=16, topk=2, sel_dim=16, causal=True, gate=True).to(DEV)
+    x = torch.randn(1, 128, 64, device=DEV)
+    w = torch.randn(1, 128, 64, device=DEV)
+    loss = lambda: (m(x).double() * w.double()).sum()  # noqa: E731
+    loss().backward()
+    p = m.sel_k[2].bias
+    gp = p.grad.clone()
+    eps = 5e-2
+    for idx in range(4):
+        with torch.no_grad():
+            p[idx] += eps
+            lp = loss().item()
+            p[idx] -= 2 * eps
+            lm = loss().item()
+            p[idx] += eps
+        num = (lp - lm) / (2 * eps)
+        _say("fd", idx, num, gp[idx].item())
+        assert abs(num - gp[idx].item()) <= 2e-2 * max(1.0, abs(num))
+
+
+def test_blocksparse_padding_and_needle_hooks():
+    from ssa_model import BlockSparseSSA
+    torch.manual_seed(3)
+    m = BlockSparseSSA(128, 2, block=64, topk=2, causal=True).to(DEV)
+    x = torch.randn(2, 1000, 128, device=DEV)          # L % block != 0: zero-padded like the reference
+    with torch.no_grad():
+        y = m(x, needle_pos=torch.tensor([5, 900], device=DEV))
+    assert y.shape == x.shape and torch.isfinite(y).all()
+    assert m.last_block_logits.shape == (2, 16)
+    assert 0.0 <= m.last_hit <= 1.0
+    xp = F.pad(x, (0, 0, 0, 24))
+    ref, sel = _module_oracle(m, xp)
+    assert_close(np64(y), ref[:, :1000], "f32", "padded module out")
+
+
+# ---------------------------------------------------------------- qwen_blocksparse
+def _ref_sdpa(q, k, v, causal=True):
+    grp = q.shape[1] // k.shape[1]
+    return F.scaled_dot_product_attention(q.float(), k.repeat_interleave(grp, 1).float(),
+                                          v.repeat_interleave(grp, 1).float(), is_causal=causal)
+
+
+@pytest.mark.parametrize("L", [256, 200])
+def test_qwen_fastpath_matches_sdpa(L):
+    from qwen_blocksparse import blocksparse_forward
+    torch.manual_seed(0)
+    B, Hq, Hkv, d = 1, 16, 2, 64
+    q, k, v = torch.randn(B, Hq, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV)
+    for causal in (True, False):
+        out = blocksparse_forward(q, k, v, selector=None, topk=9999, bs=32, causal=causal)
+        assert out.shape == (B, Hq, L, d)
+        assert torch.allclose(out, _ref_sdpa(q, k, v, causal), atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("L", [192, 200])
+def test_qwen_gather_allcausal_matches_sdpa(L):
+    from qwen_blocksparse import blocksparse_forward, SelectAll
+    torch.manual_seed(0)
+    B, Hq, Hkv, d = 1, 8, 2, 48
+    q, k, v = torch.randn(B, Hq, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV)
+    out = blocksparse_forward(q, k, v, selector=SelectAll(bs=32), topk=0, bs=32, causal=True, q_chunk=3)
+    assert out.shape == (B, Hq, L, d)
+    assert torch.allclose(out, _ref_sdpa(q, k, v), atol=1e-3, rtol=1e-3)
+
+
+def test_qwen_selectors_causal_and_budget():
+    from qwen_blocksparse import SelectMax, SelectOracle, SelectRandom, blocksparse_forward
+    torch.manual_seed(0)
+    B, Hq, Hkv, L, d = 1, 16, 2, 256, 64
+    q, k, v = torch.randn(B, Hq, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV), torch.randn(B, Hkv, L, d, device=DEV)
+    nblk = L // 32
+    qb = torch.arange(nblk, device=DEV).view(1, 1, nblk, 1)
+    for S in (SelectMax(topk=4, bs=32, sink=True), SelectRandom(topk=4, bs=32, sink=True, seed=1)):
+        idx = S.select(q, k)
+        assert idx.shape == (B, Hkv, nblk, 6) and (idx <= qb).all() and (idx >= 0).all()
+        assert (idx == 0).any(-1).all() and (idx == qb).any(-1).all()
+        assert torch.equal(idx, idx.sort(-1).values)
+        out = blocksparse_forward(q, k, v, selector=S, topk=4, bs=32, q_chunk=2)
+        assert out.shape == (B, Hq, L, d) and torch.isfinite(out).all()
+    mass = torch.rand(B, Hkv, 8, 8, device=DEV) * 0.01
+    mass[..., 0] = 1.0
+    idx = SelectOracle(topk=1, bs=32, sink=False).select_from_mass(mass)
+    assert (idx == 0).any(-1).all()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_qwen_selectmax_forward_matches_oracle_with_outgate(dtype):
+    # config-4-like: GQA 8/2, d128, bs64, Quest top-6 + own + sink, padded L, output gate
+    from qwen_blocksparse import blocksparse_forward, SelectMax
+    g = torch.Generator().manual_seed(4)
+    B, Hq, Hkv, L, d, bs, topk = 1, 8, 2, 1000, 128, 64, 6
+    q, og = randn(g, (B, Hq, L, d), dtype), randn(g, (B, Hq, L, d), dtype)
+    k, v = randn(g, (B, Hkv, L, d), dtype), randn(g, (B, Hkv, L, d), dtype)
+    S = SelectMax(topk=topk, bs=bs, sink=True)
+    idx = S.select(q.to(DEV), k.to(DEV)).cpu().numpy()
+    Lp = 1024
+    pad = lambda t: np.pad(np64(t), ((0, 0), (0, 0), (0, Lp - L), (0, 0)))  # noqa: E731
+    ref_idx, _ = osel.select_quest(pad(q), pad(k), bs, topk, True, dtype)
+    assert np.array_equal(idx, ref_idx)
+    out = blocksparse_forward(q.to(DEV), k.to(DEV), v.to(DEV), selector=S, topk=topk, bs=bs, scale=0.1,
+                              out_gate=og.to(DEV))
+    ro, _ = oattn.fwd(pad(q), pad(k), pad(v), ref_idx, "token_causal", scale=0.1, L_valid=L, out_gate=pad(og))
+    assert_close(np64(out), ro[:, :, :L], dtype, "out")
