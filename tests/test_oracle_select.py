@@ -1,0 +1,208 @@
+"""Pins for the selection oracle (CPU).
+
+* rounding helpers against torch's own dtype conversions;
+* pooling against closed forms (constant blocks, min <= x <= max) and torch's
+  CPU reductions (``view(...).mean(3).mean(1)``, ``src/ssa_model.py:287-288``;
+  ``src/qwen_blocksparse.py:113-116``);
+* the Quest bound (``src/qwen_blocksparse.py:8-10``);
+* conventions A and B against brute-force per-row sorting and against
+  torch.topk / sort on tie-free scores (the reference's own routines,
+  ``src/ssa_model.py:151-165``, ``src/qwen_blocksparse.py:87-99``);
+* budget/causality invariants and the planted-mass check
+  (``src/test_qwen_blocksparse.py:37-71``);
+* causal-prefix invariance and the near-tie census.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as on, select as osel
+
+RNG = np.random.default_rng(0)
+
+
+# ---------------------------------------------------------------- numerics
+def test_round_bf16_matches_torch():
+    x = np.concatenate([RNG.standard_normal(100000) * 10.0 ** RNG.integers(-8, 4, 100000),
+                        # exact bf16 midpoints (ties to even) and their neighbours
+                        (np.arange(1, 2000, dtype=np.float32) * 2 ** -7 + 2 ** -8) * 3.0])
+    x32 = x.astype(np.float32)
+    ref = torch.from_numpy(x32).to(torch.bfloat16).float().numpy().astype(np.float64)
+    np.testing.assert_array_equal(on.round_bf16(x32.astype(np.float64)), ref)
+    ref16 = torch.from_numpy(x32).to(torch.float16).float().numpy().astype(np.float64)
+    np.testing.assert_array_equal(on.round_f16(x32.astype(np.float64)), ref16)
+    np.testing.assert_array_equal(on.round_f32(x), x.astype(np.float32).astype(np.float64))
+
+
+def test_round_bf16_double_rounding_point():
+    # torch rounds an fp32 accumulator; a float64 value just above a bf16
+    # midpoint that rounds to the midpoint in fp32 must then tie to even
+    mid = 1.0 + 2 ** -8                   # midpoint between 1 and 1 + 2^-7
+    x = mid + 2 ** -40                    # rounds to exactly `mid` in fp32
+    assert on.round_bf16(np.array([x]))[0] == 1.0
+    assert on.round_bf16(np.array([mid + 2 ** -20]))[0] == 1.0 + 2 ** -7
+
+
+# ---------------------------------------------------------------- pooling
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_pool_mean_matches_torch_cpu(dtype):
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    B, H, N, D, bs = 2, 4, 512, 32, 64
+    x = torch.randn(B, H, N, D, generator=torch.Generator().manual_seed(1)).to(tdt)
+    ref = x.view(B, H, N // bs, bs, D).mean(3).mean(1).double().numpy()
+    got = osel.pool_mean_tok_then_heads(x.double().numpy(), bs, dtype)
+    # torch's CPU accumulator may differ from the exact sum in the last fp32 bits;
+    # a different bf16 result is only possible at a rounding midpoint (1 ulp)
+    ref2 = x.view(B, 2, 2, N // bs, bs, D).mean(2).mean(3).double().numpy()   # SelectMax's order
+    got2 = osel.pool_mean_grp_then_tok(x.double().numpy(), 2, bs, dtype)
+    for g_, r_ in ((got, ref), (got2, ref2)):
+        if dtype == "bf16":
+            diff = g_ != r_
+            assert diff.mean() < 2e-3
+            ulp = 2.0 ** (np.floor(np.log2(np.abs(r_[diff]))) - 7)
+            assert np.all(np.abs(g_[diff] - r_[diff]) <= ulp)
+        else:
+            # the oracle is the exactly rounded mean; torch's fp32 accumulator is within a few ulps
+            np.testing.assert_allclose(g_, r_, rtol=4e-7 * 64, atol=1e-8)
+
+
+def test_pool_closed_forms():
+    B, H, N, D, bs = 1, 2, 96, 8, 32
+    c = RNG.standard_normal((B, H, N // bs, 1, D))
+    x = np.broadcast_to(c, (B, H, N // bs, bs, D)).reshape(B, H, N, D)
+    x = on.round_bf16(x)
+    pm = osel.pool_mean_tok_then_heads(x, bs, "bf16")
+    np.testing.assert_array_equal(pm, on.round_bf16(x.reshape(B, H, -1, bs, D)[:, :, :, 0].mean(1)))
+    k = RNG.standard_normal((B, H, N, D))
+    kmin, kmax = osel.pool_minmax(k, bs)
+    kb = k.reshape(B, H, N // bs, bs, D)
+    assert np.all(kmin[:, :, :, None] <= kb) and np.all(kb <= kmax[:, :, :, None])
+    assert np.all((kb == kmin[:, :, :, None]).any(3)) and np.all((kb == kmax[:, :, :, None]).any(3))
+    # zero padding takes part (src/qwen_blocksparse.py:112-116)
+    kmin2, kmax2 = osel.pool_minmax(k[:, :, :80], bs)
+    assert np.all(kmin2[:, :, 2] <= 0) and np.all(kmax2[:, :, 2] >= 0)
+    tk = torch.from_numpy(k)
+    np.testing.assert_array_equal(kmax, tk.view(B, H, -1, bs, D).max(3).values.numpy())
+
+
+def test_quest_score_upper_bounds_token_products():
+    B, Hq, Hkv, N, D, bs = 1, 4, 2, 128, 16, 16
+    q = RNG.standard_normal((B, Hq, N, D))
+    k = RNG.standard_normal((B, Hkv, N, D))
+    qpool = osel.pool_mean_grp_then_tok(q, Hkv, bs, "f32")
+    kmin, kmax = osel.pool_minmax(k, bs)
+    exact = (np.maximum(qpool, 0)[..., :, None, :] * kmax[..., None, :, :]
+             + np.minimum(qpool, 0)[..., :, None, :] * kmin[..., None, :, :]).sum(-1)
+    kb = k.reshape(B, Hkv, N // bs, bs, D)
+    prod = np.einsum("bhid,bhjsd->bhijs", qpool, kb).max(-1)      # max_s qpool_i . k_s over block j
+    assert np.all(exact >= prod - 1e-12)
+    sc = osel.scores(qpool, kmax, "f32", "quest", b2=kmin)
+    np.testing.assert_allclose(sc, exact, rtol=1e-6, atol=1e-6)
+
+
+def test_scores_match_torch_matmul_rounding():
+    a = on.round_bf16(RNG.standard_normal((2, 40, 32)))
+    b = on.round_bf16(RNG.standard_normal((2, 40, 32)))
+    ta, tb = (torch.from_numpy(x).to(torch.bfloat16) for x in (a, b))
+    ref = (ta @ tb.transpose(-1, -2)).double().numpy()
+    got = osel.scores(a, b, "bf16", "dot")
+    assert (got != ref).mean() < 5e-3      # only accumulator-order midpoints may differ
+    b2 = on.round_bf16(RNG.standard_normal((2, 40, 32)))
+    ref2 = torch.maximum(ta @ tb.transpose(-1, -2), ta @ torch.from_numpy(b2).to(torch.bfloat16).transpose(-1, -2))
+    assert (osel.scores(a, b, "bf16", "max2", b2=b2) != ref2.double().numpy()).mean() < 5e-3
+
+
+# ---------------------------------------------------------------- conventions
+def _brute_a(raw_row, i, topk, causal):
+    nblk = len(raw_row)
+    cand = [j for j in range(nblk) if j != i and (not causal or j < i)]
+    cand.sort(key=lambda j: (-raw_row[j], j))
+    kk_c = min(topk, nblk - 1)
+    picks = cand[:kk_c]
+    return [i] + picks + [i] * (kk_c - len(picks))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_convention_a_bruteforce_with_ties(causal):
+    raw = np.round(RNG.standard_normal((2, 23, 23)) * 2) / 2     # many exact ties
+    for topk in (0, 1, 5, 22, 40):
+        sel = osel.select_conv_a(raw, topk, causal)
+        for b in range(2):
+            for i in range(23):
+                assert sel[b, i].tolist() == _brute_a(raw[b, i], i, topk, causal)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_convention_a_matches_torch_topk(causal):
+    # the reference's selection code path on tie-free scores
+    nblk, topk = 50, 7
+    raw = torch.from_numpy(RNG.standard_normal((3, nblk, nblk)))
+    diag = torch.arange(nblk)
+    content = raw.clone()
+    content[:, diag, diag] = float("-inf")
+    if causal:
+        content = content.masked_fill((diag.view(nblk, 1) < diag.view(1, nblk)).unsqueeze(0), float("-inf"))
+    sel_ref = torch.cat([diag.view(1, nblk, 1).expand(3, nblk, 1), content.topk(topk, dim=-1).indices], -1).numpy()
+    sel = osel.select_conv_a(raw.numpy(), topk, causal)
+    valid = np.isfinite(np.take_along_axis(content.numpy(), sel_ref, -1))
+    valid[..., 0] = True
+    np.testing.assert_array_equal(np.where(valid, sel, -1), np.where(valid, sel_ref, -1))
+
+
+def test_convention_b_matches_torch_finish():
+    B, H, nblk = 2, 3, 40
+    score = torch.from_numpy(RNG.standard_normal((B, H, nblk, nblk)))
+    for topk, sink in ((4, True), (4, False), (45, True)):
+        ar = torch.arange(nblk)
+        sc = score.masked_fill(ar.view(1, 1, nblk, 1) < ar.view(1, 1, 1, nblk), float("-inf"))
+        k = min(topk, nblk)
+        tv, ti = sc.topk(k, dim=-1)
+        own = ar.view(1, 1, nblk, 1).expand(B, H, nblk, 1)
+        ti = torch.where(torch.isfinite(tv), ti, own.expand_as(ti))
+        parts = [ti, own] + ([torch.zeros(B, H, nblk, 1, dtype=torch.long)] if sink else [])
+        ref = torch.cat(parts, -1).sort(-1).values.numpy()
+        got = osel.select_conv_b(score.numpy(), topk, sink)
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_convention_invariants_and_planted_mass():
+    B, H, nblk = 1, 2, 16
+    score = RNG.standard_normal((B, H, nblk, nblk))
+    idx = osel.select_conv_b(score, 4, True)
+    qb = np.arange(nblk)[None, None, :, None]
+    assert idx.shape == (B, H, nblk, 6) and np.all(idx <= qb) and np.all(idx >= 0)
+    assert np.all(np.diff(idx, axis=-1) >= 0) and np.all((idx == 0).any(-1)) and np.all((idx == qb).any(-1))
+    mass = RNG.random((B, H, 8, 8)) * 0.01
+    mass[..., 0] = 1.0
+    assert np.all((osel.select_conv_b(mass, 1, False) == 0).any(-1))
+    raw = RNG.standard_normal((B, nblk, nblk))
+    sel = osel.select_conv_a(raw, 5, True)
+    assert np.all(sel[..., 0] == np.arange(nblk))
+    content = sel[..., 1:]
+    rows = np.arange(nblk)[None, :, None]
+    assert np.all((content < rows) | (content == rows))     # fills are the own block
+    for i in range(6, nblk):                                 # enough past blocks: distinct, all past
+        assert len(set(content[0, i].tolist())) == 5 and np.all(content[0, i] < i)
+
+
+def test_causal_prefix_invariance():
+    # rows i < n' depend only on blocks <= i: selection on a prefix equals the full run's rows
+    q = RNG.standard_normal((1, 4, 64 * 40, 16))
+    k = RNG.standard_normal((1, 4, 64 * 40, 16))
+    full, _ = osel.select_mean_pooled(q, k, 64, 6, True, "bf16")
+    pre, _ = osel.select_mean_pooled(q[:, :, :64 * 25], k[:, :, :64 * 25], 64, 6, True, "bf16")
+    np.testing.assert_array_equal(full[:, :25], pre)
+    rows = np.array([3, 17, 24])
+    qp = osel.pool_mean_tok_then_heads(q, 64, "bf16")
+    kp = osel.pool_mean_tok_then_heads(k, 64, "bf16")
+    part = osel.select_conv_a(osel.scores(qp, kp, "bf16", "dot", rows=rows), 6, True, rows=rows)
+    np.testing.assert_array_equal(part, full[:, rows])
+
+
+def test_near_tie_census():
+    score = np.array([[[5.0, 3.0, 3.0 + 1e-9, 1.0, 2.0]]])
+    valid = np.ones_like(score, dtype=bool)
+    assert osel.near_tie_rows(score, np.array([[[0, 1]]]), 2, valid)[0, 0]
+    assert not osel.near_tie_rows(score, np.array([[[0, 4]]]), 2, valid)[0, 0]
+    score2 = np.array([[[5.0, 3.0, 2.5, 1.0, 2.0]]])
+    assert not osel.near_tie_rows(score2, np.array([[[0, 1]]]), 2, valid)[0, 0]
