@@ -42,7 +42,21 @@ def parse():
     p.add_argument("--bwd", action="store_true", help="also time the backward (separate fields)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-rows", type=int, default=128, help="query blocks in the CPU sample")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     return p.parse_args()
+
+
+def calibrate_copy():
+    """A plain copy of known size: 1 GiB read + 1 GiB written per launch. Its
+    FETCH_SIZE / WRITE_SIZE readings give the counter-to-byte factor."""
+    import torch
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": 1 << 30, "launches": 3}), flush=True)
 
 
 def traffic_from_profiles(kernel, workload):
@@ -98,6 +112,9 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
+    if a.calibrate_copy:
+        calibrate_copy()
+        return
     import torch
     from fbsa_amd import ops, selection
 

@@ -14,6 +14,8 @@
 // Reference semantics: src/triton_kernel.py:20-74 (online softmax over an
 // index list, slot-0 triu, future content blocks masked, gate after scale) and
 // src/qwen_blocksparse.py:67-81 (token-causal, padding, duplicate masks).
+#include <stdlib.h>
+
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
 
@@ -26,18 +28,24 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #define FBSA_FWD_LDS_BUDGET 32768
 #endif
 
-template <typename T, int BS, int D> struct FwdCfg {
+// QT: 16-query tiles per wave (each wave owns 16*QT query rows, so a WG has
+// BS/(16*QT) waves). KCO / NSO override the key-chunk size and the ring depth
+// (0 = derived).
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0> struct FwdCfg {
   static constexpr int ES = sizeof(T);
-  static constexpr int NW = BS / 16;
+  static constexpr int NW = BS / (16 * QT);
   static constexpr int NT = NW * 64;
-  static constexpr int KC = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
+  static constexpr int KC0 = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
+  static constexpr int KC = KCO ? KCO : KC0;
   static constexpr int NCH = BS / KC;
   static constexpr int CPR = D * ES / 16;
   static constexpr int TILE_BYTES = KC * D * ES;
   static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
   static constexpr int LPT = STAGE_BYTES / (NT * 16);
   static constexpr int NS0 = FBSA_FWD_LDS_BUDGET / STAGE_BYTES;
-  static constexpr int NSTAGE = NS0 < 1 ? 1 : (NS0 > 4 ? 4 : NS0);
+  static constexpr int NSTAGE = NSO ? NSO : (NS0 < 2 ? 2 : (NS0 > 4 ? 4 : NS0));
+  static_assert(NW >= 1, "block too small for the query tiling");
+  static_assert(NSTAGE >= 2, "the single-barrier ring needs two stages");
   static_assert(LPT * NT * 16 == STAGE_BYTES, "stage must split evenly over threads");
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
 };
@@ -48,13 +56,15 @@ template <int N> __device__ __forceinline__ void wait_pending(int pending_chunks
     case 0: wait_vmcnt<0>(); break;
     case 1: wait_vmcnt<(N < 64 ? N : 63)>(); break;
     case 2: wait_vmcnt<(2 * N < 64 ? 2 * N : 63)>(); break;
-    default: wait_vmcnt<(3 * N < 64 ? 3 * N : 63)>(); break;
+    case 3: wait_vmcnt<(3 * N < 64 ? 3 * N : 63)>(); break;
+    case 4: wait_vmcnt<(4 * N < 64 ? 4 * N : 63)>(); break;
+    default: wait_vmcnt<(5 * N < 64 ? 5 * N : 63)>(); break;
   }
 }
 
-template <typename T, int BS, int D>
-__global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
-  using C = FwdCfg<T, BS, D>;
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
+__global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
+  using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
   constexpr bool F32 = sizeof(T) == 4;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
@@ -63,9 +73,9 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
   float *s_gate = (float *)(s_kind + a.kk);
   __shared__ int s_nvalid;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, p = lane & 15;
   const int64_t total = a.B * a.Hq * a.nblk;
-  int64_t t = xcd_remap(blockIdx.x, total);
+  int64_t t = a.order ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, total);
   const int hin = (int)(t % a.grp); t /= a.grp;
   const int64_t i = t % a.nblk; t /= a.nblk;
   const int hk = (int)(t % a.Hkv);
@@ -109,56 +119,88 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
     if (lane == 0) s_nvalid = nout;
   }
 
-  // ---- 2. Q fragment (B operand of S^T = K Q^T) ----
-  const int tq = w * 16 + p;  // query row within the block
-  const T *qrow = (const T *)a.q + b * a.sq[0] + hq * a.sq[1] + (i * BS + tq) * a.sq[2];
+  // ---- 2. Q fragments (B operands of S^T = K Q^T), one per query tile ----
+  int tq[QT];  // query rows (within the block) of this lane's columns
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) tq[qt] = (w * QT + qt) * 16 + p;
   constexpr int QF = F32 ? D / 4 : D / 32;
-  s16x8 qf16[F32 ? 1 : QF];
-  float qf32[F32 ? QF : 1];
-  if constexpr (F32) {
+  s16x8 qf16[QT][F32 ? 1 : QF];
+  float qf32[QT][F32 ? QF : 1];
 #pragma unroll
-    for (int ks = 0; ks < QF; ++ks) qf32[ks] = ((const float *)qrow)[4 * ks + g];
-  } else {
+  for (int qt = 0; qt < QT; ++qt) {
+    const T *qrow = (const T *)a.q + b * a.sq[0] + hq * a.sq[1] + (i * BS + tq[qt]) * a.sq[2];
+    if constexpr (F32) {
 #pragma unroll
-    for (int ks = 0; ks < QF; ++ks) qf16[ks] = *(const s16x8 *)(qrow + 32 * ks + 8 * g);
+      for (int ks = 0; ks < QF; ++ks) qf32[qt][ks] = ((const float *)qrow)[4 * ks + g];
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < QF; ++ks) qf16[qt][ks] = *(const s16x8 *)(qrow + 32 * ks + 8 * g);
+    }
+  }
+
+  // Direct-to-LDS copy plan: this thread's LPT 16-byte loads of a K/V chunk.
+  // Which tensor a load reads is uniform across a wave (a tile is a whole
+  // number of 1 KiB wave-loads); the per-lane byte offset from the chunk's first
+  // row is fixed, so each issue is a scalar base plus a precomputed offset.
+  int32_t doff[C::LPT];
+#pragma unroll
+  for (int n = 0; n < C::LPT; ++n) {
+    const int wl = n * C::NW + w;
+    const int u = wl * 64 + lane;
+    const int part = u / (C::KC * C::CPR);
+    const int rem = u - part * (C::KC * C::CPR);
+    const int row = rem / C::CPR, pos = rem % C::CPR;
+    const int chunk = pos ^ swz(row, C::CPR);
+    doff[n] = (int32_t)(((int64_t)row * (part ? a.sv[2] : a.sk[2]) + chunk * (16 / C::ES)) * C::ES);
   }
   __syncthreads();
   const int nv = s_nvalid;
   const int nchunks = nv * C::NCH;
 
-  const T *kbase = (const T *)a.k + b * a.sk[0] + hk * a.sk[1];
-  const T *vbase = (const T *)a.v + b * a.sv[0] + hk * a.sv[1];
+  const char *kbase = (const char *)((const T *)a.k + b * a.sk[0] + hk * a.sk[1]);
+  const char *vbase = (const char *)((const T *)a.v + b * a.sv[0] + hk * a.sv[1]);
+  const int64_t kstep = a.sk[2] * C::ES, vstep = a.sv[2] * C::ES;
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int64_t row0 = (int64_t)s_blk[slot] * BS + ch * C::KC;
+    const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(s_blk[slot] * BS + ch * C::KC);
+    const char *kb = kbase + row0 * kstep, *vb = vbase + row0 * vstep;
     char *st = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
 #pragma unroll
     for (int n = 0; n < C::LPT; ++n) {
-      const int wl = n * C::NW + w;  // wave-load index within the stage (1 KiB each)
-      const int u = wl * 64 + lane;
-      const int part = u / (C::KC * C::CPR);
-      const int rem = u - part * (C::KC * C::CPR);
-      const int row = rem / C::CPR, pos = rem % C::CPR;
-      const int chunk = pos ^ swz(row, C::CPR);
-      const T *src = part ? vbase + (row0 + row) * a.sv[2] : kbase + (row0 + row) * a.sk[2];
-      g2lds16(src + chunk * (16 / C::ES), st + wl * 1024);
+      const bool part = (n * C::NW + w) * 64 >= C::KC * C::CPR;  // wave-uniform
+      g2lds16((part ? vb : kb) + doff[n], st + (n * C::NW + w) * 1024);
     }
   };
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 oacc[D / 16];
+  // Online softmax in the log2 domain with a lazily moved reference max: the
+  // accumulators are rescaled only when a score exceeds the reference by more
+  // than TAU (so p <= 2^TAU); each lane checks its own scores and only when
+  // one does is the per-query chunk max formed across lanes.
+  constexpr float TAU = 8.f;
+  float m_run[QT], l_run[QT];
+  f32x4 oacc[QT][D / 16];
+  f32x4 lacc[QT];  // 16-bit types: row sums of P from the PV MFMA (a tile of ones)
 #pragma unroll
-  for (int mt = 0; mt < D / 16; ++mt) oacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+    lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < D / 16; ++mt) oacc[qt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
 #pragma unroll
   for (int c = 0; c < C::NSTAGE - 1; ++c)
     if (c < nchunks) issue(c);
 
   for (int c = 0; c < nchunks; ++c) {
-    if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+    // chunk c has landed once at most min(ahead, NSTAGE-2) later chunks are in flight
     const int ahead = nchunks - 1 - c;
-    wait_pending<C::LPT>(ahead < C::NSTAGE - 1 ? ahead : C::NSTAGE - 1);
+    wait_pending<C::LPT>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
+    // one barrier per chunk: every wave has landed its part of chunk c and
+    // finished reading chunk c-1, whose stage the prefetch below overwrites
     lds_barrier();
+    if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
 
     const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
     const char *Vs = Ks + C::TILE_BYTES;
@@ -167,23 +209,46 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
     const float gt = s_gate[slot];
     const int64_t j = s_blk[slot];
 
-    // S^T (KC keys x 16 queries of this wave)
-    f32x4 sacc[C::KC / 16];
+    // V^T fragments for the PV product, shared by the query tiles; issued first
+    // so their LDS latency overlaps the score MFMAs and the softmax
+    constexpr int KV2 = C::KC >= 32 ? C::KC / 32 : 1;
+    s16x4 vlo[F32 ? 1 : D / 16][KV2], vhi[F32 ? 1 : D / 16][KV2];
+    if constexpr (!F32) {
+#pragma unroll
+      for (int mt = 0; mt < D / 16; ++mt) {
+        const int cb = 2 * mt + ((p & 3) >> 1);  // logical 16-B chunk of d0 = 16mt + 4(p&3)
+#pragma unroll
+        for (int k2 = 0; k2 < KV2; ++k2) {
+          const int ra = 32 * k2 + 4 * g + (p >> 2);
+          vlo[mt][k2] = lds_read_tr16(Vs + (ra * C::CPR + (cb ^ swz(ra, C::CPR))) * 16 + (p & 1) * 8);
+          if constexpr (C::KC >= 32) {
+            const int rb = ra + 16;
+            vhi[mt][k2] = lds_read_tr16(Vs + (rb * C::CPR + (cb ^ swz(rb, C::CPR))) * 16 + (p & 1) * 8);
+          }
+        }
+      }
+    }
+
+    // S^T (KC keys x 16 queries per tile); each K fragment feeds every tile
+    f32x4 sacc[QT][C::KC / 16];
 #pragma unroll
     for (int m = 0; m < C::KC / 16; ++m) {
-      sacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
       const int row = 16 * m + p;
       if constexpr (F32) {
 #pragma unroll
         for (int ks = 0; ks < QF; ++ks) {
           const float kf = *(const float *)(Ks + (row * C::CPR + (ks ^ swz(row, C::CPR))) * 16 + g * 4);
-          sacc[m] = mfma_f32_16x16x4(kf, qf32[ks], sacc[m]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = mfma_f32_16x16x4(kf, qf32[qt][ks], sacc[qt][m]);
         }
       } else {
 #pragma unroll
         for (int ks = 0; ks < QF; ++ks) {
           const s16x8 kf = *(const s16x8 *)(Ks + (row * C::CPR + ((4 * ks + g) ^ swz(row, C::CPR))) * 16);
-          sacc[m] = Mfma16<T>::run(kf, qf16[ks], sacc[m]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = Mfma16<T>::run(kf, qf16[qt][ks], sacc[qt][m]);
         }
       }
     }
@@ -191,157 +256,172 @@ __global__ __launch_bounds__(BS * 4) void fwd_kernel(FwdArgs a) {
     // mask: key row u (within block j) is valid iff u <= lim (uniform branch
     // skips the compares for unmasked chunks, the common case)
     if (kind != KIND_FULL) {
-      const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
-                            : kind == KIND_PAD  ? a.l_valid - j * BS - 1
-                                                : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
-                                                                                              : a.l_valid - j * BS - 1);
-      const int lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;  // compare against 16m + r
 #pragma unroll
-      for (int m = 0; m < C::KC / 16; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (16 * m + r > lim) sacc[m][r] = -INFINITY;
-    }
-    // online softmax in the log2 domain; scale and gate are folded into one
-    // FMA per score: p = exp2(s * scale2 + (gate2 - m))
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int m = 0; m < C::KC / 16; ++m)
-      mloc = fmaxf(mloc, fmaxf(fmaxf(sacc[m][0], sacc[m][1]), fmaxf(sacc[m][2], sacc[m][3])));
-    mloc = fmaxf(mloc, shfl_xor_f(mloc, 16));
-    mloc = fmaxf(mloc, shfl_xor_f(mloc, 32));
-    const float mchunk = mloc * a.scale2 + gt;  // -inf when every key is masked
-    const float m_new = fmaxf(m_run, mchunk);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    const float off = gt - m_use;
-    float sv[C::KC / 16][4];
-    float psum = 0.f;
-#pragma unroll
-    for (int m = 0; m < C::KC / 16; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off));
-        sv[m][r] = e;
-        psum += e;
-      }
-    l_run = __builtin_fmaf(l_run, alpha, psum);
-    m_run = m_new;
-    if (__ballot(alpha != 1.f)) {  // rescale only when some row max moved
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) oacc[mt][r] *= alpha;
-    }
-
-    // O^T += V^T P^T
-    if constexpr (F32) {
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt)
+      for (int qt = 0; qt < QT; ++qt) {
+        const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq[qt]
+                              : kind == KIND_PAD  ? a.l_valid - j * BS - 1
+                                                  : ((i - j) * BS + tq[qt] < a.l_valid - j * BS - 1
+                                                         ? (i - j) * BS + tq[qt]
+                                                         : a.l_valid - j * BS - 1);
+        const int lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;  // compare against 16m + r
 #pragma unroll
         for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int vrow = 16 * m + 4 * g + r;
-            const float vf = *(const float *)(Vs + (vrow * C::CPR + ((4 * mt + (p >> 2)) ^ swz(vrow, C::CPR))) * 16 + (p & 3) * 4);
-            oacc[mt] = mfma_f32_16x16x4(vf, sv[m][r], oacc[mt]);
-          }
-    } else if constexpr (C::KC >= 32) {
-      s16x8 pf[C::KC / 32];
-#pragma unroll
-      for (int k2 = 0; k2 < C::KC / 32; ++k2) {
-        float x[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { x[r] = sv[2 * k2][r]; x[4 + r] = sv[2 * k2 + 1][r]; }
-        pf[k2] = pack8<T>(x);
-      }
-      s16x4 vlo[D / 16][C::KC / 32], vhi[D / 16][C::KC / 32];
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt) {
-        const int cb = 2 * mt + ((p & 3) >> 1);  // logical 16-B chunk of d0 = 16mt + 4(p&3)
-#pragma unroll
-        for (int k2 = 0; k2 < C::KC / 32; ++k2) {
-          const int ra = 32 * k2 + 4 * g + (p >> 2);
-          const int rb = ra + 16;
-          vlo[mt][k2] = lds_read_tr16(Vs + (ra * C::CPR + (cb ^ swz(ra, C::CPR))) * 16 + (p & 1) * 8);
-          vhi[mt][k2] = lds_read_tr16(Vs + (rb * C::CPR + (cb ^ swz(rb, C::CPR))) * 16 + (p & 1) * 8);
-        }
-      }
-      lds_wait_all();
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt)
-#pragma unroll
-        for (int k2 = 0; k2 < C::KC / 32; ++k2) {
-          lds_ready(vlo[mt][k2]);
-          lds_ready(vhi[mt][k2]);
-          const s16x4 lo = vlo[mt][k2], hi = vhi[mt][k2];
-          const s16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          oacc[mt] = Mfma16<T>::run(vf, pf[k2], oacc[mt]);
-        }
-    } else {
-      // KC == 16: one 16x16x16 MFMA per d tile
-      s16x4 pf;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pf[r] = bits16<T>((T)sv[0][r]);
-      s16x4 vf[D / 16];
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt) {
-        const int cb = 2 * mt + ((p & 3) >> 1);
-        const int ra = 4 * g + (p >> 2);
-        vf[mt] = lds_read_tr16(Vs + (ra * C::CPR + (cb ^ swz(ra, C::CPR))) * 16 + (p & 1) * 8);
-      }
-      lds_wait_all();
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt) {
-        lds_ready(vf[mt]);
-        oacc[mt] = Mfma16<T>::run16(vf[mt], pf, oacc[mt]);
+          for (int r = 0; r < 4; ++r)
+            if (16 * m + r > lim) sacc[qt][m][r] = -INFINITY;
       }
     }
-    lds_barrier();  // the next iteration's prefetch overwrites this stage
+
+    // lazy reference max
+    float lmax[QT];
+    bool need = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = fmaxf(fmaxf(sacc[qt][0][0], sacc[qt][0][1]), fmaxf(sacc[qt][0][2], sacc[qt][0][3]));
+#pragma unroll
+      for (int m = 1; m < C::KC / 16; ++m)
+        mx = fmaxf(fmaxf(mx, fmaxf(sacc[qt][m][0], sacc[qt][m][1])), fmaxf(sacc[qt][m][2], sacc[qt][m][3]));
+      lmax[qt] = mx * a.scale2 + gt;  // -inf when every key of the lane is masked
+      need |= lmax[qt] > m_run[qt] + TAU;
+    }
+    if (__ballot(need)) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mc = fmaxf(lmax[qt], shfl_xor_f(lmax[qt], 16));
+        mc = fmaxf(mc, shfl_xor_f(mc, 32));            // the query's chunk max, same on its 4 lanes
+        if (mc > m_run[qt] + TAU) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - mc);  // 0 when m_run = -inf
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) lacc[qt][r] *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < D / 16; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) oacc[qt][mt][r] *= alpha;
+          m_run[qt] = mc;
+        }
+      }
+    }
+
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float off = gt - (m_run[qt] == -INFINITY ? 0.f : m_run[qt]);
+      float sv[C::KC / 16][4];
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv[m][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qt][m][r], a.scale2, off));
+
+      // O^T += V^T P^T (and, for 16-bit types, the row sums of P as one more tile)
+      if constexpr (F32) {
+        float psum = 0.f;
+#pragma unroll
+        for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) psum += sv[m][r];
+        l_run[qt] += psum;
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt)
+#pragma unroll
+          for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int vrow = 16 * m + 4 * g + r;
+              const float vf = *(const float *)(Vs + (vrow * C::CPR + ((4 * mt + (p >> 2)) ^ swz(vrow, C::CPR))) * 16 + (p & 3) * 4);
+              oacc[qt][mt] = mfma_f32_16x16x4(vf, sv[m][r], oacc[qt][mt]);
+            }
+      } else if constexpr (C::KC >= 32) {
+        constexpr short ONE = (short)(__is_same(T, bf16) ? 0x3F80 : 0x3C00);
+        const s16x8 ones = {ONE, ONE, ONE, ONE, ONE, ONE, ONE, ONE};
+        s16x8 pf[C::KC / 32];
+#pragma unroll
+        for (int k2 = 0; k2 < C::KC / 32; ++k2) {
+          float x[8];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) { x[r] = sv[2 * k2][r]; x[4 + r] = sv[2 * k2 + 1][r]; }
+          pf[k2] = pack8<T>(x);
+          lacc[qt] = Mfma16<T>::run(ones, pf[k2], lacc[qt]);
+        }
+        if (qt == 0) lds_wait_all();
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt)
+#pragma unroll
+          for (int k2 = 0; k2 < C::KC / 32; ++k2) {
+            lds_ready(vlo[mt][k2]);
+            lds_ready(vhi[mt][k2]);
+            const s16x4 lo = vlo[mt][k2], hi = vhi[mt][k2];
+            const s16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            oacc[qt][mt] = Mfma16<T>::run(vf, pf[k2], oacc[qt][mt]);
+          }
+      } else {
+        // KC == 16: one 16x16x16 MFMA per d tile
+        constexpr short ONE = (short)(__is_same(T, bf16) ? 0x3F80 : 0x3C00);
+        const s16x4 ones = {ONE, ONE, ONE, ONE};
+        s16x4 pf;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pf[r] = bits16<T>((T)sv[0][r]);
+        lacc[qt] = Mfma16<T>::run16(ones, pf, lacc[qt]);
+        if (qt == 0) lds_wait_all();
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt) {
+          lds_ready(vlo[mt][0]);
+          oacc[qt][mt] = Mfma16<T>::run16(vlo[mt][0], pf, oacc[qt][mt]);
+        }
+      }
+    }
   }
 
   // ---- 4. epilogue ----
-  float lt = l_run + shfl_xor_f(l_run, 16);
-  lt += shfl_xor_f(lt, 32);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  T *orow = (T *)a.o + b * a.so[0] + hq * a.so[1] + (i * BS + tq) * a.so[2];
-  const T *ogrow = a.og ? (const T *)a.og + b * a.sog[0] + hq * a.sog[1] + (i * BS + tq) * a.sog[2] : nullptr;
 #pragma unroll
-  for (int mt = 0; mt < D / 16; ++mt) {
-    const int d0 = 16 * mt + 4 * g;
-    float y[4];
+  for (int qt = 0; qt < QT; ++qt) {
+    float lt;
+    if constexpr (F32) {
+      lt = l_run[qt] + shfl_xor_f(l_run[qt], 16);
+      lt += shfl_xor_f(lt, 32);
+    } else {
+      lt = lacc[qt][0];  // every row of the ones-tile holds the full sum for query p
+    }
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    T *orow = (T *)a.o + b * a.so[0] + hq * a.so[1] + (i * BS + tq[qt]) * a.so[2];
+    const T *ogrow = a.og ? (const T *)a.og + b * a.sog[0] + hq * a.sog[1] + (i * BS + tq[qt]) * a.sog[2] : nullptr;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = oacc[mt][r] * inv;
-    if (ogrow) {
+    for (int mt = 0; mt < D / 16; ++mt) {
+      const int d0 = 16 * mt + 4 * g;
+      float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float z = to_f32<T>(ogrow[d0 + r]);
-        y[r] *= 1.f / (1.f + __expf(-z));
+      for (int r = 0; r < 4; ++r) y[r] = oacc[qt][mt][r] * inv;
+      if (ogrow) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float z = to_f32<T>(ogrow[d0 + r]);
+          y[r] *= 1.f / (1.f + __expf(-z));
+        }
+      }
+      if constexpr (F32) {
+        *(f32x4 *)(orow + d0) = f32x4{y[0], y[1], y[2], y[3]};
+      } else {
+        s16x4 pk;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)y[r]);
+        *(s16x4 *)(orow + d0) = pk;
       }
     }
-    if constexpr (F32) {
-      *(f32x4 *)(orow + d0) = f32x4{y[0], y[1], y[2], y[3]};
-    } else {
-      s16x4 pk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)y[r]);
-      *(s16x4 *)(orow + d0) = pk;
+    if (a.lse && g == 0) {
+      const int64_t li = (b * a.Hq + hq) * a.L + i * BS + tq[qt];
+      a.lse[li] = lt > 0.f ? (m_run[qt] + __log2f(lt)) * kLn2 : -INFINITY;
     }
-  }
-  if (a.lse && g == 0) {
-    const int64_t li = (b * a.Hq + hq) * a.L + i * BS + tq;
-    a.lse[li] = lt > 0.f ? (m_run + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }
 
-template <typename T, int BS, int D> static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
-  using C = FwdCfg<T, BS, D>;
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
+static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
+  using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (size_t)a.kk * 12;
   if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: kk=%lld needs %zu bytes of LDS", (long long)a.kk, lds);
   if (lds > 64 * 1024) {
     static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation
     if (lds > attr_bytes) {
-      int e = hip_check(hipFuncSetAttribute((const void *)fwd_kernel<T, BS, D>,
+      int e = hip_check(hipFuncSetAttribute((const void *)fwd_kernel<T, BS, D, QT, KCO, NSO>,
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                         "hipFuncSetAttribute(fwd)");
       if (e) return e;
@@ -349,11 +429,28 @@ template <typename T, int BS, int D> static int launch_fwd(const FwdArgs &a, hip
     }
   }
   const int64_t nwg = a.B * a.Hq * a.nblk;
-  hipLaunchKernelGGL((fwd_kernel<T, BS, D>), dim3((unsigned)nwg), dim3(C::NT), lds, stream, a);
+  hipLaunchKernelGGL((fwd_kernel<T, BS, D, QT, KCO, NSO>), dim3((unsigned)nwg), dim3(C::NT), lds, stream, a);
   return hip_check(hipGetLastError(), "fwd_kernel launch");
 }
 
+static int fwd_variant() {
+  static const int v = [] {
+    const char *e = getenv("FBSA_FWD_CFG");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
 template <typename T, int BS> static int dispatch_d(const FwdArgs &a, int64_t D, hipStream_t s) {
+  if constexpr (sizeof(T) == 2 && BS == 64) {
+    if (D == 64) switch (fwd_variant()) {
+      case 1: return launch_fwd<T, BS, 64, 1, 64, 3>(a, s);
+      case 2: return launch_fwd<T, BS, 64, 2>(a, s);
+      case 3: return launch_fwd<T, BS, 64, 2, 64, 3>(a, s);
+      case 4: return launch_fwd<T, BS, 64, 4>(a, s);
+      case 5: return launch_fwd<T, BS, 64, 2, 32, 4>(a, s);
+    }
+  }
   switch (D) {
     case 32: return launch_fwd<T, BS, 32>(a, s);
     case 64: return launch_fwd<T, BS, 64>(a, s);
@@ -373,7 +470,13 @@ template <typename T> static int dispatch_bs(const FwdArgs &a, int64_t bs, int64
   return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: block size %lld not in {16,32,64,128}", (long long)bs);
 }
 
-int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s) {
+int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a0, hipStream_t s) {
+  static const int order = [] {
+    const char *e = getenv("FBSA_FWD_ORDER");
+    return e ? atoi(e) : 0;
+  }();
+  FwdArgs a = a0;
+  a.order = order;
   switch (d->dtype) {
     case FBSA_BF16: return dispatch_bs<bf16>(a, d->bs, d->D, s);
     case FBSA_F16: return dispatch_bs<f16>(a, d->bs, d->D, s);

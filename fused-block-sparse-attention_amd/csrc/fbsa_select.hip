@@ -86,6 +86,31 @@ template <typename T> __device__ __forceinline__ void load8(const T *p, double *
   }
 }
 
+// Raw 8-element row chunk (kept undecoded until used, to keep registers low).
+template <typename T> struct Raw8 {
+  uint4 w[sizeof(T) == 4 ? 2 : 1];
+};
+template <typename T> __device__ __forceinline__ Raw8<T> load_raw8(const T *p) {
+  Raw8<T> r;
+  r.w[0] = *(const uint4 *)p;
+  if constexpr (sizeof(T) == 4) r.w[1] = *(const uint4 *)(p + 4);
+  return r;
+}
+template <typename T> __device__ __forceinline__ void decode8(const Raw8<T> &r, double *v) {
+  const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+  if constexpr (sizeof(T) == 4) {
+    const uint32_t w2[4] = {r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = (double)__uint_as_float(w[e]); v[4 + e] = (double)__uint_as_float(w2[e]); }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = (double)half_bits_to_f32<T>(w[e] & 0xFFFFu);
+      v[2 * e + 1] = (double)half_bits_to_f32<T>(w[e] >> 16);
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
   __shared__ double red[256 * 8];   // per-thread partial results (8 d values)
@@ -230,6 +255,177 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
   }
 }
 
+// Wave-organised pooling for a block of BS tokens and D/8 = DC a power of two
+// <= 64: a wave covers whole rows (DC lanes per row, 64/DC rows at a time),
+// every lane keeps eight exact fp64 sums, and row partials meet by in-wave
+// xor-shuffles; only the four wave partials go through LDS. Each lane's loads
+// are issued back to back (fixed trip count; rows past l_valid are read at a
+// clamped address and contribute 0). MEAN_TOK_THEN_GRP gives each wave whole
+// heads; the other ops split the block's tokens over the waves.
+template <typename T, int DC, int BS, int OP>
+__global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
+  constexpr int NW = 4, TLW = 64 / DC;
+  constexpr int RPH = BS >= TLW ? BS / TLW : 1;            // rows per lane per head (whole block in one wave)
+  constexpr int RPW = BS >= NW * TLW ? BS / (NW * TLW) : 1;  // rows per lane when the waves split the block
+  __shared__ double red[2][NW][DC][8];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane % DC, tl = lane / DC;
+  const int64_t blk = blockIdx.x;
+  const int64_t i = blk % a.nblk;
+  const int64_t ho = (blk / a.nblk) % a.Ho;
+  const int64_t b = blk / (a.nblk * a.Ho);
+  constexpr int op = OP;
+  const int64_t nval = a.l_valid - i * BS < BS ? a.l_valid - i * BS : BS;  // valid tokens in the block (>= 1)
+  auto rowptr = [&](int64_t h, int t) {
+    const int tc = t < nval ? t : (int)nval - 1;
+    return (const T *)a.x + b * a.sx[0] + h * a.sx[1] + (i * BS + tc) * a.sx[2] + 8 * c;
+  };
+  auto xor_sum = [&](double *v) {
+#pragma unroll
+    for (int off = DC; off < 64; off <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += __shfl_xor(v[e], off, 64);
+  };
+
+  double r0[8], r1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { r0[e] = 0.0; r1[e] = 0.0; }
+  if constexpr (op == FBSA_POOL_MEAN_TOK_THEN_GRP) {
+    // wave w: heads w, w + 4, ...; per head an exact token sum and its rounded mean
+    for (int64_t hh = w; hh < a.grp; hh += NW) {
+      double acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = 0.0;
+      constexpr int NB = RPH < 8 ? RPH : 8;  // rows loaded back to back per batch
+      for (int n0 = 0; n0 < RPH; n0 += NB) {
+        Raw8<T> raw[NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) raw[n] = load_raw8<T>(rowptr(ho * a.grp + hh, tl + (n0 + n) * TLW));
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+          const int t = tl + (n0 + n) * TLW;
+          const bool ok = t < nval && t < BS;
+          double v[8];
+          decode8<T>(raw[n], v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += ok ? v[e] : 0.0;
+        }
+      }
+      xor_sum(acc);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r0[e] += (double)round_dt<T>(acc[e] / (double)BS);
+    }
+  } else if constexpr (op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
+    // tokens split over waves and lanes; per token an exact group sum, rounded mean
+    for (int n = 0; n < RPW; ++n) {
+      const int t = (w + n * NW) * TLW + tl;
+      double g[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[e] = 0.0;
+#pragma unroll 8
+      for (int64_t hh = 0; hh < a.grp; ++hh) {
+        double v[8];
+        load8<T>(rowptr(ho * a.grp + hh, t), v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] += v[e];
+      }
+      const bool ok = t < nval && t < BS;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r0[e] += ok ? (double)round_dt<T>(g[e] / (double)a.grp) : 0.0;
+    }
+    xor_sum(r0);
+  } else {
+    // per-block min / max over tokens; padding tokens count as 0
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { r0[e] = INFINITY; r1[e] = -INFINITY; }
+    constexpr int NB = RPW < 8 ? RPW : 8;
+    for (int n0 = 0; n0 < RPW; n0 += NB) {
+      Raw8<T> raw[NB];
+#pragma unroll
+      for (int n = 0; n < NB; ++n) raw[n] = load_raw8<T>(rowptr(ho, (w + (n0 + n) * NW) * TLW + tl));
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const int t = (w + (n0 + n) * NW) * TLW + tl;
+        if (t >= BS) continue;
+        const bool ok = t < nval;
+        double v[8];
+        decode8<T>(raw[n], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const double x = ok ? v[e] : 0.0;
+          r0[e] = fmin(r0[e], x);
+          r1[e] = fmax(r1[e], x);
+        }
+      }
+    }
+#pragma unroll
+    for (int off = DC; off < 64; off <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        r0[e] = fmin(r0[e], __shfl_xor(r0[e], off, 64));
+        r1[e] = fmax(r1[e], __shfl_xor(r1[e], off, 64));
+      }
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { red[0][w][c][e] = r0[e]; red[1][w][c][e] = r1[e]; }
+  }
+  __syncthreads();
+  if (tid < DC * 8) {
+    const int cc = tid >> 3, e = tid & 7;
+    const int64_t off = ((b * a.Ho + ho) * a.nblk + i) * a.D + 8 * cc + e;
+    if (op == FBSA_POOL_MEAN_TOK_THEN_GRP || op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
+      double tot = 0.0;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) tot += red[0][ww][cc][e];
+      const double den = op == FBSA_POOL_MEAN_TOK_THEN_GRP ? (double)a.grp : (double)BS;
+      ((T *)a.out)[off] = (T)round_dt<T>(tot / den);
+    } else {
+      double mn = red[0][0][cc][e], mx = red[1][0][cc][e];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) { mn = fmin(mn, red[0][ww][cc][e]); mx = fmax(mx, red[1][ww][cc][e]); }
+      if (a.op == FBSA_POOL_MAX) ((T *)a.out)[off] = (T)(float)mx;
+      else if (a.op == FBSA_POOL_MIN) ((T *)a.out)[off] = (T)(float)mn;
+      else { ((T *)a.out)[off] = (T)(float)mn; ((T *)a.out2)[off] = (T)(float)mx; }
+    }
+  }
+}
+
+template <typename T, int DC, int BS> static void launch_pool_op(const PoolArgs &a, int64_t nwg, hipStream_t s) {
+  switch (a.op) {
+    case FBSA_POOL_MEAN_TOK_THEN_GRP:
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_TOK_THEN_GRP>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      return;
+    case FBSA_POOL_MEAN_GRP_THEN_TOK:
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_GRP_THEN_TOK>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      return;
+    default:  // MAX / MIN / MINMAX share one instantiation (the op picks the outputs)
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MINMAX>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      return;
+  }
+}
+
+template <typename T, int DC> static bool launch_pool_bs(const PoolArgs &a, int64_t nwg, hipStream_t s) {
+  switch (a.bs) {
+    case 16: launch_pool_op<T, DC, 16>(a, nwg, s); return true;
+    case 32: launch_pool_op<T, DC, 32>(a, nwg, s); return true;
+    case 64: launch_pool_op<T, DC, 64>(a, nwg, s); return true;
+    case 128: launch_pool_op<T, DC, 128>(a, nwg, s); return true;
+  }
+  return false;
+}
+
+template <typename T> static void launch_pool(const PoolArgs &a, int64_t nwg, hipStream_t s) {
+  bool done = false;
+  switch (a.D / 8) {
+    case 2: done = a.D == 16 && launch_pool_bs<T, 2>(a, nwg, s); break;
+    case 4: done = a.D == 32 && launch_pool_bs<T, 4>(a, nwg, s); break;
+    case 8: done = a.D == 64 && launch_pool_bs<T, 8>(a, nwg, s); break;
+    case 16: done = a.D == 128 && launch_pool_bs<T, 16>(a, nwg, s); break;
+    case 32: done = a.D == 256 && launch_pool_bs<T, 32>(a, nwg, s); break;
+  }
+  if (!done) hipLaunchKernelGGL(pool_kernel<T>, dim3((unsigned)nwg), dim3(256), 0, s, a);
+}
+
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s) {
   PoolArgs a;
   a.x = x; a.out = out; a.out2 = out2;
@@ -238,9 +434,9 @@ int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipS
   for (int k = 0; k < 3; ++k) a.sx[k] = d->sx[k];
   const int64_t nwg = a.B * a.Ho * a.nblk;
   switch (d->dtype) {
-    case FBSA_BF16: hipLaunchKernelGGL(pool_kernel<bf16>, dim3((unsigned)nwg), dim3(256), 0, s, a); break;
-    case FBSA_F16: hipLaunchKernelGGL(pool_kernel<f16>, dim3((unsigned)nwg), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(pool_kernel<float>, dim3((unsigned)nwg), dim3(256), 0, s, a); break;
+    case FBSA_BF16: launch_pool<bf16>(a, nwg, s); break;
+    case FBSA_F16: launch_pool<f16>(a, nwg, s); break;
+    default: launch_pool<float>(a, nwg, s); break;
   }
   return hip_check(hipGetLastError(), "pool_kernel launch");
 }
@@ -270,22 +466,28 @@ __device__ __forceinline__ float key_score(uint64_t k) {
 }
 __device__ __forceinline__ int key_index(uint64_t k) { return (int)(~(uint32_t)k); }
 
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  const uint32_t lo = __shfl((int)(uint32_t)v, src, 64), hi = __shfl((int)(uint32_t)(v >> 32), src, 64);
+// Wave-uniform lane read (src is the same for every lane): v_readlane, no LDS.
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v) {
-  const uint32_t lo = __shfl_up((int)(uint32_t)v, 1, 64), hi = __shfl_up((int)(uint32_t)(v >> 32), 1, 64);
-  return ((uint64_t)hi << 32) | lo;
+// Lane l receives lane l-1's value (lane 0 keeps its own): DPP wave_shr:1.
+__device__ __forceinline__ uint64_t wave_shr1_u64(uint64_t v) {
+  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+  const uint32_t slo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, 0x138, 0xF, 0xF, false);
+  const uint32_t shi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, 0x138, 0xF, 0xF, false);
+  return ((uint64_t)shi << 32) | slo;
 }
 
-// Insert key c into the distributed descending list (lane l holds entry l;
-// 0 = empty). K = capacity (<= 64). Keys are unique (the index is in them).
+// Insert key c (wave-uniform) into the distributed descending list (lane l
+// holds entry l; 0 = empty). K = capacity (<= 64). Keys are unique (the index
+// is part of them).
 __device__ __forceinline__ void list_insert(uint64_t &mine, uint64_t c, int lane, int K) {
   const uint64_t better = __ballot(mine > c);  // empties (0) are never better
   const int pos = __popcll(better);
   if (pos >= K) return;
-  const uint64_t prev = shfl_up_u64(mine);
+  const uint64_t prev = wave_shr1_u64(mine);
   if (lane > pos && lane < K) mine = prev;
   if (lane == pos) mine = c;
 }
@@ -363,12 +565,12 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
       else cand = cand && j <= i;
       const uint64_t key = make_key(sc, (int)j);
       // reject against the current K-th key (list entry K-1)
-      const uint64_t kth = shfl_u64(lst[r], K > 0 ? K - 1 : 0);
+      const uint64_t kth = readlane_u64(lst[r], K > 0 ? K - 1 : 0);
       uint64_t surv = __ballot(cand && key > kth);
       while (surv) {
         const int src = __ffsll((unsigned long long)surv) - 1;
         surv &= surv - 1;
-        const uint64_t c = shfl_u64(key, src);
+        const uint64_t c = readlane_u64(key, src);
         list_insert(lst[r], c, lane, K);
       }
     }
@@ -393,7 +595,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
     float *scrow = a.sel_score ? a.sel_score + (bh * a.nblk + i) * a.kk : nullptr;
     if (convA) {
       // slot 0 = own block; slots 1..K = list order; missing picks -> own
-      const uint64_t prev = shfl_up_u64(mine);
+      const uint64_t prev = wave_shr1_u64(mine);
       if (lane < a.kk) {
         int idx = (int)i;
         float sc = dsc;
@@ -414,7 +616,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
       const int n = (int)a.kk;
       int rank = 0;
       for (int m = 0; m < n; ++m) {
-        const int om = __shfl(idx, m, 64);
+        const int om = __builtin_amdgcn_readlane(idx, m);
         rank += (om < idx) || (om == idx && m < lane);
       }
       if (lane < n) {
