@@ -116,17 +116,17 @@ int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, voi
   return run_pool(d, x, out, out2, (hipStream_t)stream);
 }
 
-size_t fbsa_select_workspace_bytes(const fbsa_select_desc *) { return 0; }
+size_t fbsa_select_workspace_bytes(const fbsa_select_desc *d) { return d ? select_workspace_bytes(d) : 0; }
 
 int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
                 float *sel_score, void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace; (void)workspace_bytes;
   if (!d) return fail(FBSA_EINVAL, "fbsa_select: null descriptor");
   if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_select: bad dtype %d", d->dtype);
   if (d->score < FBSA_SCORE_DOT || d->score > FBSA_SCORE_QUEST) return fail(FBSA_EINVAL, "fbsa_select: bad score %d", d->score);
   if (d->convention != FBSA_SEL_OWN_FIRST && d->convention != FBSA_SEL_SORTED_SINK)
     return fail(FBSA_EINVAL, "fbsa_select: bad convention %d", d->convention);
   if (d->B < 1 || d->H < 1 || d->nblk < 1 || d->topk < 0) return fail(FBSA_EINVAL, "fbsa_select: bad sizes");
+  if (d->flags & ~(0xFFFF << FBSA_SEL_CHUNK_SHIFT)) return fail(FBSA_EINVAL, "fbsa_select: unknown flags 0x%x", d->flags);
   int64_t K, kk;
   if (d->convention == FBSA_SEL_OWN_FIRST) { K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1; kk = 1 + K; }
   else { K = d->topk < d->nblk ? d->topk : d->nblk; kk = K + 1 + (d->sink ? 1 : 0); }
@@ -138,7 +138,11 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
     return fail(FBSA_EINVAL, "fbsa_select: misaligned pointer");
   const int64_t ntile = (d->nblk + 7) / 8;
   if (ntile * d->B * d->H > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select: grid too large");
-  return run_select(d, a, b1, b2, sel, sel_score, (hipStream_t)stream);
+  // the workspace enables the MFMA path; without one the fp64 kernel runs (same results)
+  const size_t need = select_workspace_bytes(d);
+  void *ws = (workspace && workspace_bytes >= need && need > 0) ? workspace : nullptr;
+  if (ws && !aligned(ws, 16)) return fail(FBSA_EINVAL, "fbsa_select: workspace must be 16-byte aligned");
+  return run_select(d, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

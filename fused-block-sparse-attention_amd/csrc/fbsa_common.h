@@ -52,6 +52,17 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
+// Wait until at most `pending` ring stages of N direct-to-LDS loads each are
+// still in flight (the loads of older stages have landed).
+template <int N> __device__ __forceinline__ void wait_ring(int pending) {
+  switch (pending) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<(N < 64 ? N : 63)>(); break;
+    case 2: wait_vmcnt<(2 * N < 64 ? 2 * N : 63)>(); break;
+    default: wait_vmcnt<(3 * N < 64 ? 3 * N : 63)>(); break;
+  }
+}
+
 // Workgroup barrier for LDS-staged pipelines. Unlike __syncthreads() it does
 // not wait for outstanding vector-memory ops (which would drain the
 // direct-to-LDS prefetch ring); callers wait for their own DMA with

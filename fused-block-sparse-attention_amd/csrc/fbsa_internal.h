@@ -25,8 +25,9 @@ struct FwdArgs {
 
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
+size_t select_workspace_bytes(const fbsa_select_desc *d);
 int run_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
-               float *sel_score, hipStream_t s);
+               float *sel_score, void *ws, hipStream_t s);
 
 // ---- backward ----
 // Byte offsets of the backward workspace regions (each 256-byte aligned).

@@ -446,7 +446,10 @@ struct SelArgs {
   const void *a, *b1, *b2;
   int32_t *sel;
   float *sel_score;
+  const float *an1, *an2, *bn1, *bn2;  // row norms (MFMA path): query-side parts and key-side operands
+  uint64_t *part;                      // MFMA path: per-(row, candidate chunk) top-k keys
   int64_t B, H, nblk, D, topk, kk;
+  int64_t ct, nch;                     // MFMA path: candidate tiles per chunk, chunks per row block
   int conv, causal, sink, score;
 };
 
@@ -627,41 +630,793 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
   }
 }
 
-template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, hipStream_t s) {
+// ------------------------------------------------ MFMA selection (16-bit operands)
+//
+// Scores come from bf16/fp16 MFMA (fp32 accumulate). With exact 16-bit
+// products, the fp32 result differs from the exact dot product by at most
+// beta = 4 (D + 4) 2^-24 |a| |b| (any summation order, round-to-nearest or
+// toward zero, plus the final fp32 rounding), so rounding r - beta and
+// r + beta to the score dtype brackets the exactly rounded score (rounding is
+// monotone):
+//   * a candidate whose upper end lies below the row's reject boundary (the
+//     rounding midpoint under its current k-th score) cannot enter the row's
+//     top-k and is dropped with one compare -- almost every candidate once the
+//     row has a k-th score;
+//   * a survivor whose bracket collapses has its exact score; otherwise the
+//     score is recomputed exactly in fp64 from the 16-bit operands (rare).
+// Survivors are appended to a per-row buffer; a full buffer is compacted to
+// its top k by a wave-wide bitonic sort of (score, complemented index) keys,
+// which also raises the reject boundary. Keys order exactly as in the fp64
+// kernel, so the selected blocks and their tie-break are identical.
+//
+// Work split: a workgroup takes 64 query rows (16 per wave, one MFMA tile
+// each) and one chunk of candidate tiles (64 candidates), streamed through a
+// two-stage direct-to-LDS ring shared by the waves. Rows with more than one
+// chunk leave per-chunk top-k keys that select_merge_kernel combines.
+
+// bf16 bit pattern of the smallest bf16 value >= x (x >= 0, +inf or NaN).
+__device__ __forceinline__ uint32_t bf16_up_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u & 0xFFFFu) u = (u + 0x10000u) & 0xFFFF0000u;
+  return u >> 16;
+}
+// max(m, x) ignoring a NaN x (IEEE maxNum); one instruction.
+__device__ __forceinline__ float vmax(float m, float x) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(x));
+  return r;
+}
+
+// Norm arrays hold nbp = nblk rounded up to 64 entries per (batch, head), so a
+// 64-candidate tile of norms is one aligned run; the padding is never used.
+__host__ __device__ static inline int64_t sel_norm_pitch(int64_t nblk) { return (nblk + 63) & ~(int64_t)63; }
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void sel_norms_kernel(SelArgs a, float *an1, float *an2, float *bn1, float *bn2) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = a.B * a.H * a.nblk;
+  if (row >= n) return;
+  const int64_t nrow = row / a.nblk * sel_norm_pitch(a.nblk) + row % a.nblk;
+  const T *A = (const T *)a.a + row * D;
+  const T *B1 = (const T *)a.b1 + row * D;
+  const T *B2 = MODE != FBSA_SCORE_DOT ? (const T *)a.b2 + row * D : nullptr;
+  double sa1 = 0.0, sa2 = 0.0, sb1 = 0.0, sb2 = 0.0;
+  for (int d0 = 0; d0 < D; d0 += 8) {
+    double v[8], w1[8], w2[8];
+    load8<T>(A + d0, v);
+    load8<T>(B1 + d0, w1);
+    if (MODE != FBSA_SCORE_DOT) load8<T>(B2 + d0, w2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (MODE == FBSA_SCORE_QUEST) {
+        if (v[e] > 0.0) sa1 += v[e] * v[e];
+        else sa2 += v[e] * v[e];
+      } else {
+        sa1 += v[e] * v[e];
+      }
+      sb1 += w1[e] * w1[e];
+      if (MODE != FBSA_SCORE_DOT) sb2 += w2[e] * w2[e];
+    }
+  }
+  // Norms rounded up (the bounds must not shrink). Norms outside
+  // [2^-40, 1e18] become +inf: every pair they touch then has no usable
+  // bound (inf or NaN) and reaches the exact path; this keeps the MFMA
+  // accumulation away from fp32 overflow and underflow. Key-side norms are
+  // stored rounded up to bf16, the precision of the rank-1 MFMA term.
+  auto sane = [](double ss) -> float {
+    if (ss == 0.0) return 0.f;
+    const double nrm = sqrt(ss) * (1.0 + 1e-6);
+    return nrm >= 0x1p-40 && nrm <= 1e18 ? (float)nrm : INFINITY;
+  };
+  an1[nrow] = sane(sa1);
+  an2[nrow] = sane(sa2);
+  bn1[nrow] = __uint_as_float(bf16_up_bits(sane(sb1)) << 16);
+  bn2[nrow] = __uint_as_float(bf16_up_bits(sane(sb2)) << 16);
+}
+
+// Wave-wide bitonic sort of 64 keys (one per lane), descending.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
+      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
+      const uint64_t pv = ((uint64_t)hi << 32) | lo;
+      const bool desc = (lane & k) == 0;    // this lane's run is sorted descending
+      const bool lower = (lane & j) == 0;   // this lane holds the first element of the pair
+      const bool keep_max = lower == desc;
+      v = keep_max ? (v > pv ? v : pv) : (v < pv ? v : pv);
+    }
+  return v;
+}
+
+// Largest fp32 value below which every value rounds (in T) to less than s:
+// the midpoint between s and the next smaller T value.
+template <typename T> __device__ __forceinline__ float reject_boundary(float s) {
+  if (!(s > -INFINITY)) return -INFINITY;  // -inf or NaN: nothing can be rejected
+  if (s == INFINITY) return s;
+  if constexpr (__is_same(T, bf16)) {
+    uint32_t u = __float_as_uint(s);
+    // next smaller bf16: step the 16-bit pattern down (toward -inf)
+    uint32_t prev;
+    if (s == 0.f) prev = 0x80010000u;  // -smallest subnormal bf16
+    else if (u & 0x80000000u) prev = u + 0x10000u;
+    else prev = u - 0x10000u;
+    return (float)(((double)s + (double)__uint_as_float(prev)) * 0.5);
+  } else {
+    const _Float16 h = (_Float16)s;
+    unsigned short b;
+    __builtin_memcpy(&b, &h, 2);
+    unsigned short pb;
+    if (s == 0.f) pb = 0x8001;
+    else if (b & 0x8000) pb = (unsigned short)(b + 1);
+    else pb = (unsigned short)(b - 1);
+    _Float16 ph;
+    __builtin_memcpy(&ph, &pb, 2);
+    return (float)(((double)s + (double)(float)ph) * 0.5);
+  }
+}
+
+// Exact score of (query row i, candidate j), rounded like torch, from the
+// operands in global memory (fp64 products and sum).
+template <typename T, int D, int MODE>
+__device__ float exact_score_global(const SelArgs &a, int64_t bh, int64_t i, int64_t j) {
+  const T *A = (const T *)a.a + (bh * a.nblk + i) * D;
+  float part[2] = {0.f, 0.f};
+  const int nop = MODE == FBSA_SCORE_DOT ? 1 : 2;
+  for (int op = 0; op < nop; ++op) {
+    const T *Bj = (const T *)(op ? a.b2 : a.b1) + (bh * a.nblk + j) * D;
+    double acc = 0.0;
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      double av[8], bv[8];
+      load8<T>(A + d0, av);
+      load8<T>(Bj + d0, bv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        double x = av[e];
+        if (MODE == FBSA_SCORE_QUEST) x = op == 0 ? (x > 0.0 ? x : 0.0) : (x < 0.0 ? x : 0.0);
+        acc = __builtin_fma(x, bv[e], acc);
+      }
+    }
+    part[op] = round_dt<T>(acc);
+  }
+  if (MODE == FBSA_SCORE_DOT) return part[0];
+  if (MODE == FBSA_SCORE_MAX2) return fmaxf(part[0], part[1]);
+  return round_dt_f<T>(part[0] + part[1]);
+}
+
+// Writes a row's selection from its top-K keys (lane l holds the l-th best;
+// 0 = none): own-first (convention A) or _finish (convention B).
+template <typename T, int D, int MODE>
+__device__ void emit_row(const SelArgs &a, int64_t bh, int64_t i, uint64_t mine, int lane, int K) {
+  const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
+  int32_t *srow = a.sel + (bh * a.nblk + i) * a.kk;
+  float *scrow = a.sel_score ? a.sel_score + (bh * a.nblk + i) * a.kk : nullptr;
+  float dsc = 0.f, ssc = 0.f;
+  if (scrow) {
+    dsc = exact_score_global<T, D, MODE>(a, bh, i, i);
+    if (!convA && a.sink) ssc = exact_score_global<T, D, MODE>(a, bh, i, 0);
+  }
+  if (convA) {
+    const uint64_t prev = wave_shr1_u64(mine);
+    if (lane < a.kk) {
+      int idx = (int)i;
+      float sc = dsc;
+      if (lane >= 1 && prev != 0) { idx = key_index(prev); sc = key_score(prev); }
+      srow[lane] = idx;
+      if (scrow) scrow[lane] = sc;
+    }
+  } else {
+    int idx = (int)i;
+    float sc = dsc;
+    if (lane < K) {
+      if (mine != 0) {
+        const float v = key_score(mine);
+        if (isfinite(v)) { idx = key_index(mine); sc = v; }
+      }
+    } else if (lane == K + 1 && a.sink) { idx = 0; sc = ssc; }
+    const int n = (int)a.kk;
+    int rank = 0;
+    for (int m = 0; m < n; ++m) {
+      const int om = __builtin_amdgcn_readlane(idx, m);
+      rank += (om < idx) || (om == idx && m < lane);
+    }
+    if (lane < n) {
+      srow[rank] = idx;
+      if (scrow) scrow[rank] = sc;
+    }
+  }
+}
+
+template <typename T, int D, int MODE> struct SelTCfg {
+  static constexpr int KS = D / 32;
+  static constexpr int NOP = MODE == FBSA_SCORE_DOT ? 1 : 2;
+  static constexpr int CPR = D * 2 / 16;         // 16-byte chunks per candidate row
+  static constexpr int OPB = 64 * D * 2;         // one operand tile (64 candidates)
+  static constexpr int NRMB = NOP * 64 * 4;      // the tile's candidate norms
+  static constexpr int STB = NOP * OPB + NRMB;   // one ring stage
+  static constexpr int LPT = NOP * OPB / (256 * 16);
+  static constexpr int CAP = 64;                 // per-row key buffer
+  static constexpr int NST = NOP * OPB <= 8192 ? 4 : 2;  // ring depth: about 74 KB of LDS, 2 workgroups per CU
+  static constexpr int OFF_BUF = NST * STB;
+  static constexpr int OFF_QRAW = OFF_BUF + 64 * (CAP + 1) * 8;
+  static constexpr int OFF_ROWN = OFF_QRAW + 64 * D * 2;
+  static constexpr int OFF_CNT = OFF_ROWN + 2 * 64 * 4;
+  static constexpr int LDS = OFF_CNT + 64 * 4;
+  static_assert(LPT * 256 * 16 == NOP * OPB, "stage must split evenly over threads");
+};
+
+// LDS fetch-and-add, returning the old value. Inline asm: the compiler's
+// atomic waits for every outstanding direct-to-LDS load first.
+__device__ __forceinline__ int lds_fetch_add(int *p, int v) {
+  int r;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(r)
+               : "v"((unsigned)(uintptr_t)p), "v"(v)
+               : "memory");
+  return r;
+}
+
+// Register grids indexed by per-lane values: a binary tree of selects on the
+// index bits (a chain of compares against 1, 2, 3 gets turned into indexed
+// scratch memory).
+__device__ __forceinline__ float pick4(float v0, float v1, float v2, float v3, int i) {
+  const float lo = (i & 1) ? v1 : v0, hi = (i & 1) ? v3 : v2;
+  return (i & 2) ? hi : lo;
+}
+__device__ __forceinline__ float pick4(const float (&v)[4], int i) { return pick4(v[0], v[1], v[2], v[3], i); }
+__device__ __forceinline__ float pick16(const f32x4 (&v)[4], int t, int r) {
+  return pick4(pick4(v[0][0], v[1][0], v[2][0], v[3][0], t), pick4(v[0][1], v[1][1], v[2][1], v[3][1], t),
+               pick4(v[0][2], v[1][2], v[2][2], v[3][2], t), pick4(v[0][3], v[1][3], v[2][3], v[3][3], t), r);
+}
+
+// Sorts, descending, four independent sets of 64 values (index r), each held
+// by a 16-lane group of the wave: element 4 p + i of set r is v[r][i] of lane
+// p of the group. The four sorts run interleaved so the lane exchanges overlap.
+__device__ __forceinline__ void group_sort64x4_desc(float (&v)[4][4], int p) {
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 4) {
+        const int lx = j >> 2;  // partner lane p ^ lx, same register
+        const bool lower = (p & lx) == 0;
+        float o[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[r][i] = __shfl_xor(v[r][i], lx, 64);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool desc = ((4 * p + i) & k) == 0;
+            v[r][i] = lower == desc ? fmaxf(v[r][i], o[r][i]) : fminf(v[r][i], o[r][i]);
+          }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (i & j) continue;
+            const bool desc = ((4 * p + i) & k) == 0;
+            const float x = v[r][i], y = v[r][i | j];
+            v[r][i] = desc ? fmaxf(x, y) : fminf(x, y);
+            v[r][i | j] = desc ? fminf(x, y) : fmaxf(x, y);
+          }
+      }
+    }
+}
+
+// Two passes over a workgroup's candidate tiles, on MFMA bounds:
+//  * each score is formed by MFMA together with a rank-1 term +-beta(i, j),
+//    beta = bf16_up(CB |a_i|) * bf16_up(|b_j|) with CB = 4 (D+8) 2^-24 (1.01):
+//    that covers the accumulation error of the D products and of the term
+//    itself, so lo(i, j) <= exact score <= hi(i, j) comes straight out of
+//    the matrix core (the norm arrays hold bf16-rounded-up values);
+//  1. per row, the maximum of lo over each of 64 candidate streams (stream =
+//     position in the tile). The K-th largest stream maximum tau is the lower
+//     end of K distinct candidates, so rnd(tau) <= the row's K-th best score,
+//     and a candidate whose hi lies below the rounding midpoint under rnd(tau)
+//     has K candidates strictly above it: it cannot be selected.
+//  2. candidates at or above that boundary get exact keys (the bracket
+//     [hi - 2.02 beta, hi] rounded, or fp64 when that is ambiguous) and go to
+//     the row's key buffer; a buffer near capacity is cut to its top K, which
+//     also raises the boundary to the midpoint under its K-th score.
+// Pass 2 keeps about K candidates per row, so the exact work and the
+// bookkeeping stay small next to the MFMA and the reject compare.
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
+  using C = SelTCfg<T, D, MODE>;
+  constexpr int NST = C::NST;
+  constexpr int NA = MODE == FBSA_SCORE_QUEST ? 2 : 1;  // query-side operand parts
+  constexpr float CB = 4.f * (float)(D + 8) * 5.9604645e-8f * 1.01f;
+  // All LDS is one dynamic block (C::LDS bytes): accesses to statically
+  // declared LDS get a wait for every outstanding direct-to-LDS load inserted
+  // before them, which would drain the prefetch ring.
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char *ring = smem;                                             // NST stages
+  auto buf = (uint64_t(*)[C::CAP + 1])(smem + C::OFF_BUF);     // per-row key buffers (padded pitch)
+  auto qraw = (short(*)[D])(smem + C::OFF_QRAW);               // query rows (fp64 fallback)
+  auto rown = (float(*)[64])(smem + C::OFF_ROWN);              // bf16_up(CB |a-part|) per row
+  int *cnt = (int *)(smem + C::OFF_CNT);                       // key buffer fill
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, p = lane & 15;
+  const int64_t nrb = (a.nblk + 63) / 64;
+  // consecutive work items (same head) on one XCD, so its L2 holds that head's candidates
+  int64_t x = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t ch = x % a.nch; x /= a.nch;
+  const int64_t rb = nrb - 1 - x % nrb;  // heavy (late) row blocks first
+  const int64_t bh = x / nrb;
+  const int64_t r0 = rb * 64;
+  const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
+  const int64_t last_row = r0 + 63 < a.nblk - 1 ? r0 + 63 : a.nblk - 1;
+  const int64_t jmax = (a.causal || !convA) ? last_row : a.nblk - 1;
+  const int64_t ntiles = jmax / 64 + 1;
+  const int64_t nchunks = (ntiles + a.ct - 1) / a.ct;
+  const int64_t t0 = ch * a.ct, t1 = t0 + a.ct < ntiles ? t0 + a.ct : ntiles;
+  if (t0 >= t1) return;  // uniform: this chunk is past the row block's candidates
+  const int nt = (int)(t1 - t0);
+  const int K = (int)(convA ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1) : (a.topk < a.nblk ? a.topk : a.nblk));
+
+  const T *A = (const T *)a.a + bh * a.nblk * D;
+  const char *Bop[2] = {(const char *)((const T *)a.b1 + bh * a.nblk * D),
+                        (const char *)((const T *)(MODE != FBSA_SCORE_DOT ? a.b2 : a.b1) + bh * a.nblk * D)};
+  const int64_t nbp = sel_norm_pitch(a.nblk);
+  const char *Nop[2] = {(const char *)(a.bn1 + bh * nbp), (const char *)(a.bn2 + bh * nbp)};
+  const float *Anrm[2] = {a.an1 + bh * nbp, a.an2 + bh * nbp};
+
+  // query rows (16-bit patterns) for the exact fallback, per-row beta factors
+  // and counters; MFMA A fragments of this wave's 16 rows (lane p <-> row
+  // r0 + 16w + p) and the rank-1 fragments (k = 0 held by lanes g == 0)
+  for (int e = tid; e < 64 * D / 8; e += 256) {
+    const int r = e / (D / 8), c8 = e % (D / 8);
+    const int64_t i = r0 + r < a.nblk ? r0 + r : a.nblk - 1;
+    *(s16x8 *)&qraw[r][8 * c8] = *(const s16x8 *)(A + i * D + 8 * c8);
+  }
+  if (tid < 64) cnt[tid] = 0;
+  if (tid < 64 * NA) {
+    const int r = tid & 63;
+    const int64_t i = r0 + r < a.nblk ? r0 + r : a.nblk - 1;
+    rown[tid >> 6][r] = __uint_as_float(bf16_up_bits(CB * Anrm[tid >> 6][i]) << 16);
+  }
+  s16x8 af[NA][C::KS];
+  s16x8 alo[NA], ahi[NA];
+  {
+    const int64_t ip = r0 + 16 * w + p < a.nblk ? r0 + 16 * w + p : a.nblk - 1;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      const s16x8 v = *(const s16x8 *)(A + ip * D + 32 * ks + 8 * g);
+      if constexpr (MODE == FBSA_SCORE_QUEST) {
+        s16x8 pos, neg;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool negative = v[e] < 0;  // sign bit of the 16-bit pattern
+          pos[e] = negative ? (short)0 : v[e];
+          neg[e] = negative ? v[e] : (short)0;
+        }
+        af[0][ks] = pos;
+        af[1][ks] = neg;
+      } else {
+        af[0][ks] = v;
+      }
+    }
+#pragma unroll
+    for (int oa = 0; oa < NA; ++oa) {
+      const uint32_t bb = bf16_up_bits(CB * Anrm[oa][ip]);
+      ahi[oa] = s16x8{g == 0 ? (short)bb : (short)0, 0, 0, 0, 0, 0, 0, 0};
+      alo[oa] = s16x8{g == 0 ? (short)(bb | 0x8000u) : (short)0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  // ring: LPT 16-byte loads of the operand tiles per thread plus one norm
+  // load per wave. Thread chunk n of a stage: operand (4n + w) / CPR (uniform),
+  // candidate row drow[n], byte offset doff[n] within the operand tile.
+  uint32_t doff[C::LPT];
+  int drow[C::LPT];
+#pragma unroll
+  for (int n = 0; n < C::LPT; ++n) {
+    const int u = (n * 4 + w) * 64 + lane;
+    const int rem = u % (64 * C::CPR);
+    const int row = rem / C::CPR, pos = rem % C::CPR;
+    drow[n] = row;
+    doff[n] = (uint32_t)((row * D + (pos ^ swz(row, C::CPR)) * 8) * 2);
+  }
+  auto issue = [&](int64_t tile, int stg) {
+    char *st = ring + stg * C::STB;
+    const int64_t j0 = tile * 64;
+    const int lim = (int)(a.nblk - 1 - j0 < 63 ? a.nblk - 1 - j0 : 63);  // last real candidate row
+#pragma unroll
+    for (int n = 0; n < C::LPT; ++n) {
+      const int op = (n * 4 + w) / C::CPR;
+      const char *tb = Bop[op] + j0 * D * 2;
+      const int over = drow[n] - lim;  // ragged tile: repeat the last real row
+      const uint32_t off = doff[n] - (uint32_t)(over > 0 ? over * D * 2 : 0);
+      g2lds16(tb + off, st + (n * 4 + w) * 1024);
+    }
+    // norms: wave w copies candidates 16w..16w+15 of every operand; lane l
+    // lands at byte 16 l of the wave's run, so float (w NOP + op) 16 + c
+    // holds candidate 16 w + c of operand op (the per-head arrays are padded
+    // to whole tiles)
+    if (lane < 4 * C::NOP) {
+      const int op = lane >> 2, part = lane & 3;
+      g2lds16(Nop[op] + (j0 + 16 * w + 4 * part) * 4, st + C::NOP * C::OPB + w * C::NOP * 64);
+    }
+  };
+
+  // Cuts row 16w + qq (wave-uniform) of the key buffer to its top K, in
+  // descending order, and raises the row's reject boundary.
+  float rej[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  auto compact = [&](int qq) {
+    const int q = 16 * w + qq;
+    const int n = __builtin_amdgcn_readfirstlane(cnt[q]);
+    const uint64_t key = lane < n ? buf[q][lane] : 0;
+    // rank = number of larger keys (keys are distinct), from lane reads: no LDS round trips
+    int rank = 0;
+    for (int m = 0; m < n; ++m) rank += readlane_u64(key, m) > key ? 1 : 0;
+    if (lane < n && rank < K) buf[q][rank] = key;
+    if (n >= K) {
+      const uint64_t bal = __ballot(lane < n && rank == K - 1);
+      const uint64_t kth = readlane_u64(key, (int)__builtin_ctzll(bal));
+      const float nb = reject_boundary<T>(key_score(kth));
+      if (g == (qq >> 2)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r == (qq & 3)) rej[r] = fmaxf(rej[r], nb);
+      }
+    }
+    if (lane == 0) cnt[q] = n < K ? n : K;
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+  };
+
+  // validity of (row 4g + r, candidate 16t + p) on a diagonal or ragged tile: bit 4t + r
+  const int ilim = (int)(a.nblk - r0 < 64 ? a.nblk - r0 : 64);
+  auto valid_mask = [&](int64_t tl) {
+    const int jlim = (int)(a.nblk - tl * 64 < 64 ? a.nblk - tl * 64 : 64);
+    const bool diag = tl == rb;
+    const int dm = !diag ? 0 : convA ? (a.causal ? 1 : 2) : 3;  // none, j < i, j != i, j <= i
+    uint32_t vm = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 16 * w + 4 * g + r, jl = 16 * t + p, dd = il - jl;
+        bool v = il < ilim && jl < jlim;
+        v = v && (dm == 0 || (dm == 1 && dd > 0) || (dm == 2 && dd != 0) || (dm == 3 && dd >= 0));
+        vm |= v ? 1u << (4 * t + r) : 0u;
+      }
+    return vm;
+  };
+
+  float smax[4][4];  // [t][r]: stream maxima of the lower ends
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) smax[t][r] = -INFINITY;
+
+  // stage k of the ring holds tile t0 + k % nt of pass k / nt
+  auto tile_of = [&](int k) { return t0 + (k < nt ? k : k - nt); };
+#pragma unroll
+  for (int k = 0; k < NST - 1; ++k)
+    if (k < 2 * nt) issue(tile_of(k), k);
+  for (int it = 0; it < 2 * nt; ++it) {
+    const int stg = it % NST;
+    const bool collect = it >= nt;
+    const int64_t tl = tile_of(it);
+    // this wave's loads of stage it have landed (LPT + 1 per stage; later stages may be in flight)
+    const int ahead = 2 * nt - 1 - it < NST - 2 ? 2 * nt - 1 - it : NST - 2;
+    wait_ring<C::LPT + 1>(ahead);
+    lds_barrier();  // every wave's part has landed; the stage refilled next is no longer read
+    if (it + NST - 1 < 2 * nt) issue(tile_of(it + NST - 1), (it + NST - 1) % NST);
+    if (it == nt) {
+      // pass-1 bound: K-th largest of the row's 64 stream maxima
+      float v[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[r][t] = smax[t][r];
+      group_sort64x4_desc(v, p);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float tau = __shfl(pick4(v[r], (K - 1) & 3), 16 * g + ((K - 1) >> 2), 64);
+        rej[r] = reject_boundary<T>(round_dt_f<T>(tau));
+      }
+    }
+    const char *st = ring + stg * C::STB;
+    const float *nrm = (const float *)(st + C::NOP * C::OPB);
+    const int64_t j0 = tl * 64;
+
+    // lo (pass 1) or hi (pass 2) of the wave's 16 rows x 64 candidates
+    s16x8 bfr[C::NOP][4][C::KS];
+    s16x8 bp[C::NOP][4];
+#pragma unroll
+    for (int op = 0; op < C::NOP; ++op)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = 16 * t + p;
+        const uint32_t nb = __float_as_uint(nrm[(t * C::NOP + op) * 16 + p]) >> 16;  // already bf16
+        bp[op][t] = s16x8{g == 0 ? (short)nb : (short)0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks)
+          bfr[op][t][ks] = *(const s16x8 *)(st + op * C::OPB + (row * C::CPR + ((4 * ks + g) ^ swz(row, C::CPR))) * 16);
+      }
+    f32x4 acc[C::NOP][4];
+#pragma unroll
+    for (int op = 0; op < C::NOP; ++op) {
+      const int oa = MODE == FBSA_SCORE_QUEST ? op : 0;
+      const s16x8 ar = collect ? ahi[oa] : alo[oa];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        // rank-1 term (k = 0 of an extra bf16 k-block). For bf16 operands it
+        // heads the same-opcode accumulation chain; for fp16 it is a separate
+        // product added afterwards (a chain mixing MFMA opcodes through the
+        // accumulator reads it before the first product has landed)
+        const f32x4 r1 = Mfma16<bf16>::run(ar, bp[op][t], f32x4{0.f, 0.f, 0.f, 0.f});
+        acc[op][t] = sizeof(T) == 2 && __is_same(T, bf16) ? r1 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) acc[op][t] = Mfma16<T>::run(af[oa][ks], bfr[op][t][ks], acc[op][t]);
+        if constexpr (!__is_same(T, bf16)) acc[op][t] += r1;
+      }
+    }
+    const bool masked = tl == rb || j0 + 64 > a.nblk;  // diagonal or ragged tile
+
+    if (!collect) {
+      // pass 1: stream maxima of the lower ends (a NaN end is ignored)
+      const uint32_t vm = masked ? valid_mask(tl) : 0xFFFFu;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float lo0 = acc[0][t][r], lo1 = -INFINITY;
+          if constexpr (MODE == FBSA_SCORE_QUEST) lo0 = round_dt_f<T>(acc[0][t][r]) + round_dt_f<T>(acc[1][t][r]);
+          if constexpr (MODE == FBSA_SCORE_MAX2) lo1 = acc[1][t][r];
+          if (masked && !((vm >> (4 * t + r)) & 1u)) lo0 = lo1 = -INFINITY;
+          smax[t][r] = vmax(smax[t][r], lo0);
+          if constexpr (MODE == FBSA_SCORE_MAX2) smax[t][r] = vmax(smax[t][r], lo1);
+        }
+      continue;
+    }
+
+    // pass 2: reject against the row's boundary (NaN survives)
+    bool s[4][4];
+    uint64_t any = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (MODE == FBSA_SCORE_QUEST) {
+          s[t][r] = !(round_dt_f<T>(acc[0][t][r]) + round_dt_f<T>(acc[1][t][r]) < rej[r]);
+        } else {
+          s[t][r] = !(acc[0][t][r] < rej[r]);
+          if constexpr (MODE == FBSA_SCORE_MAX2) s[t][r] = s[t][r] || !(acc[1][t][r] < rej[r]);
+        }
+        any |= __ballot(s[t][r]);
+      }
+    if (!any) continue;
+    const uint32_t vm = masked ? valid_mask(tl) : 0xFFFFu;
+    uint32_t sv = 0;  // bit 4t + r: candidate 16t + p survives for row 4g + r
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sv |= s[t][r] ? 1u << (4 * t + r) : 0u;
+    sv &= vm;
+
+    // survivors: one per lane per round, exact keys appended to the row buffers
+    while (__ballot(sv != 0)) {
+      {  // a round adds at most 16 keys to a row (one per lane of its group)
+        const int c = lane < 16 ? cnt[16 * w + lane] : 0;
+        uint64_t ov = __ballot(lane < 16 && c > C::CAP - 16);
+        while (ov) {
+          const int qq = (int)__builtin_ctzll(ov);
+          ov &= ov - 1;
+          compact(qq);
+        }
+      }
+      const bool has = sv != 0;
+      const int b = has ? __builtin_ctz(sv) : 0;
+      sv &= sv - 1;
+      if (has) {
+        const int t = b >> 2, r = b & 3;
+        const int q = 16 * w + 4 * g + r;
+        const int row = 16 * t + p;
+        float ex[2] = {0.f, 0.f};
+#pragma unroll
+        for (int op = 0; op < C::NOP; ++op) {
+          const float hi = pick16(acc[op], t, r);
+          // (beta factors from LDS: indexing the register copies by t, r would spill)
+          const float beta = rown[MODE == FBSA_SCORE_QUEST ? op : 0][q] * nrm[(t * C::NOP + op) * 16 + p];
+          const float rl = round_dt_f<T>(hi - 2.02f * beta), rh = round_dt_f<T>(hi);
+          if (rl == rh && isfinite(rh)) {
+            ex[op] = rh;
+          } else {
+            // exact fp64 dot product from the staged candidate row and the query row
+            double d = 0.0;
+            for (int c = 0; c < C::CPR; ++c) {
+              const s16x8 bv = *(const s16x8 *)(st + op * C::OPB + (row * C::CPR + (c ^ swz(row, C::CPR))) * 16);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                double av = (double)half_bits_to_f32<T>((uint32_t)(unsigned short)qraw[q][8 * c + e]);
+                if (MODE == FBSA_SCORE_QUEST) av = op == 0 ? (av > 0.0 ? av : 0.0) : (av < 0.0 ? av : 0.0);
+                d = __builtin_fma(av, (double)half_bits_to_f32<T>((uint32_t)(unsigned short)bv[e]), d);
+              }
+            }
+            ex[op] = round_dt<T>(d);
+          }
+        }
+        float sc;
+        if constexpr (MODE == FBSA_SCORE_DOT) sc = ex[0];
+        else if constexpr (MODE == FBSA_SCORE_MAX2) sc = fmaxf(ex[0], ex[1]);
+        else sc = round_dt_f<T>(ex[0] + ex[1]);
+        const int slot = lds_fetch_add(&cnt[q], 1);
+        buf[q][slot] = make_key(sc, (int)(j0 + row));
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+    }
+  }
+
+  // this chunk's top K of each row, 4 rows at a time (one per lane group):
+  // lane p ranks keys p, p + 16, p + 32, p + 48 of its row against the row's
+  // buffer and stores the top K in descending order
+#pragma unroll 1
+  for (int qb = 0; qb < 4; ++qb) {
+    const int q = 16 * w + 4 * qb + g;
+    const int n = cnt[q];
+    const int nmax = __builtin_amdgcn_readfirstlane(
+        max(max(__builtin_amdgcn_readlane(n, 0), __builtin_amdgcn_readlane(n, 16)),
+            max(__builtin_amdgcn_readlane(n, 32), __builtin_amdgcn_readlane(n, 48))));
+    uint64_t k[4];
+    int rk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      k[e] = p + 16 * e < n ? buf[q][p + 16 * e] : 0;
+      rk[e] = 0;
+    }
+    for (int m = 0; m < nmax; ++m) {
+      const uint64_t km = m < n ? buf[q][m] : 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rk[e] += km > k[e] ? 1 : 0;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (k[e] != 0 && rk[e] < K) buf[q][rk[e]] = k[e];
+    if (p == 0) cnt[q] = n < K ? n : K;
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+  }
+  const bool single = nchunks == 1;
+  for (int qq = 0; qq < 16; ++qq) {
+    const int q = 16 * w + qq;
+    const int64_t i = r0 + q;
+    if (i >= a.nblk) break;
+    const int n = __builtin_amdgcn_readfirstlane(cnt[q]);
+    const uint64_t v = lane < n ? buf[q][lane] : 0;
+    if (single) emit_row<T, D, MODE>(a, bh, i, v, lane, K);
+    else if (lane < K) a.part[((bh * a.nblk + i) * a.nch + ch) * K + lane] = v;
+  }
+}
+
+// Rows whose candidates span several chunks: merge the chunks' top-k keys.
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void select_merge_kernel(SelArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (bh, i)
+  if (row >= a.B * a.H * a.nblk) return;
+  const int64_t i = row % a.nblk, bh = row / a.nblk;
+  const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
+  const int64_t jmax = (a.causal || !convA) ? ((i / 64) * 64 + 63 < a.nblk - 1 ? (i / 64) * 64 + 63 : a.nblk - 1)
+                                            : a.nblk - 1;
+  const int64_t ntiles = jmax / 64 + 1;
+  const int64_t nchunks = (ntiles + a.ct - 1) / a.ct;
+  if (nchunks <= 1) return;
+  const int K = (int)(convA ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1) : (a.topk < a.nblk ? a.topk : a.nblk));
+  const uint64_t *src = a.part + row * a.nch * K;
+  const int64_t total = nchunks * K;
+  uint64_t v = lane < K ? src[lane] : 0;  // chunk 0 (already sorted)
+  for (int64_t off = K; off < total; off += 64 - K) {
+    const int64_t e = off + (lane - K);
+    if (lane >= K) v = e < total ? src[e] : 0;
+    v = wave_sort_desc(v, lane);
+  }
+  if (lane >= K) v = 0;
+  emit_row<T, D, MODE>(a, bh, i, v, lane, K);
+}
+
+// Candidate tiles per workgroup: about 2048 workgroups over the row blocks,
+// chunks of at least 32 tiles (each chunk pays a fixed cost for its bound and
+// its final cut); a nonzero override (descriptor flags) wins.
+static void sel_chunking(int64_t B, int64_t H, int64_t nblk, int64_t override_ct, int64_t *ct, int64_t *nch) {
+  const int64_t ntiles = (nblk + 63) / 64;
+  const int64_t rbs = B * H * ntiles;
+  int64_t c = override_ct;
+  if (c <= 0) {
+    const int64_t want = (2048 + rbs - 1) / rbs;
+    c = (ntiles + want - 1) / want;
+    if (c < 32) c = 32;
+  }
+  *ct = c;
+  *nch = (ntiles + c - 1) / c;
+}
+
+template <typename T, int D, int MODE> static bool sel_tiled_ok(const SelArgs &a) {
+  if constexpr (sizeof(T) != 2 || (D != 32 && D != 64)) return false;
+  const int64_t K = a.conv == FBSA_SEL_OWN_FIRST ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1)
+                                                 : (a.topk < a.nblk ? a.topk : a.nblk);
+  return K >= 1 && K <= 48;
+}
+
+template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, void *ws, hipStream_t s) {
+  if (ws && sel_tiled_ok<T, D, MODE>(a)) {
+    if constexpr (sizeof(T) == 2 && (D == 32 || D == 64)) {
+      const int64_t n = a.B * a.H * a.nblk;
+      const int64_t npad = a.B * a.H * sel_norm_pitch(a.nblk);
+      float *an1 = (float *)ws, *an2 = an1 + npad, *bn1 = an2 + npad, *bn2 = bn1 + npad;
+      hipLaunchKernelGGL((sel_norms_kernel<T, D, MODE>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, an1,
+                         an2, bn1, bn2);
+      int e = hip_check(hipGetLastError(), "sel_norms_kernel launch");
+      if (e) return e;
+      SelArgs b = a;
+      b.an1 = an1; b.an2 = an2; b.bn1 = bn1; b.bn2 = bn2;
+      b.part = (uint64_t *)(((uintptr_t)(bn2 + npad) + 255) & ~(uintptr_t)255);
+      const int64_t nrb = (a.nblk + 63) / 64;
+      using C = SelTCfg<T, D, MODE>;
+      hipLaunchKernelGGL((select_tiled_kernel<T, D, MODE>), dim3((unsigned)(a.B * a.H * nrb * b.nch)), dim3(256),
+                         C::LDS, s, b);
+      e = hip_check(hipGetLastError(), "select_tiled_kernel launch");
+      if (e || b.nch == 1) return e;
+      hipLaunchKernelGGL((select_merge_kernel<T, D, MODE>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, b);
+      return hip_check(hipGetLastError(), "select_merge_kernel launch");
+    }
+  }
   constexpr int R = 8;
   const int64_t ntile = (a.nblk + R - 1) / R;
   const int64_t nwg = ntile * a.B * a.H;
   hipLaunchKernelGGL((select_kernel<T, D, R, MODE>), dim3((unsigned)nwg), dim3(256), 0, s, a);
   return hip_check(hipGetLastError(), "select_kernel launch");
 }
-template <typename T, int D> static int sel_mode(const SelArgs &a, hipStream_t s) {
+template <typename T, int D> static int sel_mode(const SelArgs &a, void *ws, hipStream_t s) {
   switch (a.score) {
-    case FBSA_SCORE_DOT: return launch_sel<T, D, FBSA_SCORE_DOT>(a, s);
-    case FBSA_SCORE_MAX2: return launch_sel<T, D, FBSA_SCORE_MAX2>(a, s);
-    default: return launch_sel<T, D, FBSA_SCORE_QUEST>(a, s);
+    case FBSA_SCORE_DOT: return launch_sel<T, D, FBSA_SCORE_DOT>(a, ws, s);
+    case FBSA_SCORE_MAX2: return launch_sel<T, D, FBSA_SCORE_MAX2>(a, ws, s);
+    default: return launch_sel<T, D, FBSA_SCORE_QUEST>(a, ws, s);
   }
 }
-template <typename T> static int sel_d(const SelArgs &a, hipStream_t s) {
+template <typename T> static int sel_d(const SelArgs &a, void *ws, hipStream_t s) {
   switch (a.D) {
-    case 16: return sel_mode<T, 16>(a, s);
-    case 32: return sel_mode<T, 32>(a, s);
-    case 64: return sel_mode<T, 64>(a, s);
-    case 128: return sel_mode<T, 128>(a, s);
-    case 256: return sel_mode<T, 256>(a, s);
+    case 16: return sel_mode<T, 16>(a, ws, s);
+    case 32: return sel_mode<T, 32>(a, ws, s);
+    case 64: return sel_mode<T, 64>(a, ws, s);
+    case 128: return sel_mode<T, 128>(a, ws, s);
+    case 256: return sel_mode<T, 256>(a, ws, s);
   }
   return fail(FBSA_EUNSUPPORTED, "fbsa_select: operand dim %lld not in {16,32,64,128,256}", (long long)a.D);
 }
 
+size_t select_workspace_bytes(const fbsa_select_desc *d) {
+  // MFMA path (16-bit operands of dim 32 or 64): four padded float norm arrays
+  // and the per-(row, candidate chunk) top-k keys
+  if (d->dtype == FBSA_F32 || (d->D != 32 && d->D != 64)) return 0;
+  const int64_t n = d->B * d->H * d->nblk;
+  int64_t ct, nch;
+  sel_chunking(d->B, d->H, d->nblk, (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &ct, &nch);
+  const int64_t K = d->topk < d->nblk ? d->topk : d->nblk;
+  return (size_t)(4 * d->B * d->H * sel_norm_pitch(d->nblk)) * sizeof(float) + 256 +
+         (size_t)(n * nch * (K > 0 ? K : 1)) * sizeof(uint64_t);
+}
+
 int run_select(const fbsa_select_desc *d, const void *av, const void *b1, const void *b2, int32_t *sel,
-               float *sel_score, hipStream_t s) {
+               float *sel_score, void *ws, hipStream_t s) {
   SelArgs a;
   a.a = av; a.b1 = b1; a.b2 = b2; a.sel = sel; a.sel_score = sel_score;
+  a.an1 = a.an2 = a.bn1 = a.bn2 = nullptr;
+  a.part = nullptr;
+  sel_chunking(d->B, d->H, d->nblk, (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &a.ct, &a.nch);
   a.B = d->B; a.H = d->H; a.nblk = d->nblk; a.D = d->D; a.topk = d->topk; a.kk = d->kk;
   a.conv = d->convention; a.causal = d->causal; a.sink = d->sink; a.score = d->score;
   switch (d->dtype) {
-    case FBSA_BF16: return sel_d<bf16>(a, s);
-    case FBSA_F16: return sel_d<f16>(a, s);
-    default: return sel_d<float>(a, s);
+    case FBSA_BF16: return sel_d<bf16>(a, ws, s);
+    case FBSA_F16: return sel_d<f16>(a, ws, s);
+    default: return sel_d<float>(a, ws, s);
   }
 }
 

@@ -145,18 +145,3 @@ __device__ __forceinline__ void issue_tile_pair(char *st, const T *src0, int64_t
 }
 
 }  // namespace fbsa
-
-namespace fbsa {
-
-// Wait until at most `pending` ring stages of N direct-to-LDS loads each are
-// still in flight (the loads of older stages have landed).
-template <int N> __device__ __forceinline__ void wait_ring(int pending) {
-  switch (pending) {
-    case 0: wait_vmcnt<0>(); break;
-    case 1: wait_vmcnt<(N < 64 ? N : 63)>(); break;
-    case 2: wait_vmcnt<(2 * N < 64 ? 2 * N : 63)>(); break;
-    default: wait_vmcnt<(3 * N < 64 ? 3 * N : 63)>(); break;
-  }
-}
-
-}  // namespace fbsa

@@ -16,6 +16,7 @@ OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 POOL_MEAN_TOK_THEN_GRP, POOL_MEAN_GRP_THEN_TOK, POOL_MAX, POOL_MIN, POOL_MINMAX = 0, 1, 2, 3, 4
 SCORE_DOT, SCORE_MAX2, SCORE_QUEST = 0, 1, 2
 SEL_OWN_FIRST, SEL_SORTED_SINK = 0, 1
+SEL_CHUNK_SHIFT = 8
 FLAG_OUT_GATE = 1
 
 _i64x3 = ctypes.c_int64 * 3

@@ -54,13 +54,17 @@ def budget(convention, topk, nblk, sink=False):
 
 
 def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=True, sink=False,
-           need_scores=False):
+           need_scores=False, engine="auto", chunk_tiles=0):
     """Top-k key blocks per query block from pooled operands (B,H,nblk,D).
 
     convention 'own_first' (A, src/ssa_model.py:151-165): [i, top-k content
     blocks by descending score]; 'sorted_sink' (B, ``_finish``,
     src/qwen_blocksparse.py:87-99): top-k over j <= i, + own (+ sink 0), sorted.
     Returns sel int32 (B,H,nblk,kk) (and fp32 scores of the chosen slots).
+    engine: "auto" forms 16-bit scores on MFMA with exact verification (fp64
+    only where an MFMA bracket is ambiguous); "fp64" scores everything in fp64.
+    Both return identical blocks. chunk_tiles (tuning/tests): candidate tiles
+    of 64 blocks per workgroup on the MFMA path, 0 = chosen from the sizes.
     """
     _require_cuda(a, b1, b2)
     if a.dim() != 4 or a.shape != b1.shape or (b2 is not None and b2.shape != a.shape):
@@ -78,17 +82,21 @@ def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=
     d.convention = conv
     d.causal = 1 if causal else 0
     d.sink = 1 if sink else 0
-    d.flags = 0
+    if not 0 <= chunk_tiles < 65536:
+        raise ValueError("fbsa.select: chunk_tiles must be in [0, 65536)")
+    d.flags = chunk_tiles << _lib.SEL_CHUNK_SHIFT
     d.B, d.H, d.nblk, d.D, d.topk, d.kk = B, H, nblk, D, topk, kk
     sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
     sc = torch.empty(B, H, nblk, kk, dtype=torch.float32, device=a.device) if need_scores else None
     lib = _lib.load()
-    _lib.check(lib.fbsa_select(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(sel), _ptr(sc), None, 0, _stream()),
+    nbytes = lib.fbsa_select_workspace_bytes(d) if engine == "auto" else 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    _lib.check(lib.fbsa_select(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(sel), _ptr(sc), _ptr(ws), nbytes, _stream()),
                "fbsa_select")
     return (sel, sc) if need_scores else sel
 
 
-def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False):
+def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False, engine="auto"):
     """Synthetic-config selector: mean-pooled q.k block scores, convention A.
 
     qpool = q.view(B,H,nblk,bs,D).mean(3).mean(1) (src/ssa_model.py:287-288),
@@ -98,13 +106,14 @@ def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False):
     H = q.shape[1]
     qp = pool(q, bs, "mean_tok_then_grp", grp=H)
     kp = pool(k, bs, "mean_tok_then_grp", grp=k.shape[1])
-    out = select(qp, kp, score="dot", convention="own_first", topk=topk, causal=causal, need_scores=need_scores)
+    out = select(qp, kp, score="dot", convention="own_first", topk=topk, causal=causal, need_scores=need_scores,
+                 engine=engine)
     if need_scores:
         return out[0][:, 0], out[1][:, 0]
     return out[:, 0]
 
 
-def select_quest(q, k, bs, topk, sink=True, l_valid=None):
+def select_quest(q, k, bs, topk, sink=True, l_valid=None, engine="auto"):
     """SelectMax (src/qwen_blocksparse.py:107-121): Quest upper-bound scores
     relu(qpool).kmax + min(qpool,0).kmin per KV head, then ``_finish``.
     Returns idx (B, Hkv, nblk, kk) int32."""
@@ -112,4 +121,4 @@ def select_quest(q, k, bs, topk, sink=True, l_valid=None):
     grp = q.shape[1] // Hkv
     qpool = pool(q, bs, "mean_grp_then_tok", grp=grp, l_valid=l_valid)
     kmin, kmax = pool(k, bs, "minmax", l_valid=l_valid)
-    return select(qpool, kmax, kmin, score="quest", convention="sorted_sink", topk=topk, sink=sink)
+    return select(qpool, kmax, kmin, score="quest", convention="sorted_sink", topk=topk, sink=sink, engine=engine)

@@ -113,6 +113,11 @@ enum { FBSA_SCORE_DOT = 0, FBSA_SCORE_MAX2 = 1, FBSA_SCORE_QUEST = 2 };
  *              (src/qwen_blocksparse.py:87-99) */
 enum { FBSA_SEL_OWN_FIRST = 0, FBSA_SEL_SORTED_SINK = 1 };
 
+/* fbsa_select_desc.flags: bits 8..23 = candidate tiles (64 key blocks each)
+ * per workgroup of the MFMA path, 0 = chosen from the sizes. Tuning and tests
+ * only; the result does not depend on it. Other bits must be 0. */
+enum { FBSA_SEL_CHUNK_SHIFT = 8 };
+
 typedef struct fbsa_select_desc {
   int32_t dtype, score, convention, causal, sink, flags;
   int64_t B, H, nblk, D, topk, kk;  /* operands (B, H, nblk, D) contiguous */
@@ -120,7 +125,11 @@ typedef struct fbsa_select_desc {
 
 /* Streaming score + top-k: writes sel (B,H,nblk,kk) int32 and, when sel_score
  * != NULL, the score of each chosen slot as fp32 (for the log-sigmoid gate).
- * Ties break towards the lower block index.
+ * Ties break towards the lower block index. With a workspace of at least
+ * fbsa_select_workspace_bytes() bytes (16-byte aligned; nonzero for 16-bit
+ * operands of dim >= 32) scores are formed on MFMA and verified exactly (fp64
+ * only where the rounding is ambiguous); without one, every score is formed
+ * in fp64. Both give the same result.
  * Replaces the topk selection of src/ssa_model.py:151-165,
  * src/bench_crossover.py:41-54 and SelectMax/_finish
  * (src/qwen_blocksparse.py:87-121). */

@@ -53,6 +53,7 @@ def _check_sel(got, ref, what):
                           f"got {got[tuple(bad[0][:-1])]} ref {ref[tuple(bad[0][:-1])]}"
 
 
+@pytest.mark.parametrize("engine", ["auto", "fp64"])
 @pytest.mark.parametrize("dtype,B,H,N,bs,topk,causal", [
     ("f32", 1, 4, 4096, 64, 8, True),      # config 1
     ("bf16", 32, 8, 1024, 32, 4, True),    # config 2
@@ -60,13 +61,13 @@ def _check_sel(got, ref, what):
     ("bf16", 2, 2, 2048, 64, 5, False),    # non-causal
     ("f16", 1, 2, 2048, 32, 12, True),
 ])
-def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal):
+def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal, engine):
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(2)
     D = 64
     q, k = (randn(g, (B, H, N, D), dtype) for _ in range(2))
-    _say("mean-pooled", dtype, B, H, N, bs, topk, causal)
-    sel, sc = selection.select_mean_pooled(q.to(DEV), k.to(DEV), bs, topk, causal, need_scores=True)
+    _say("mean-pooled", dtype, B, H, N, bs, topk, causal, engine)
+    sel, sc = selection.select_mean_pooled(q.to(DEV), k.to(DEV), bs, topk, causal, need_scores=True, engine=engine)
     ref, raw = osel.select_mean_pooled(np64(q), np64(k), bs, topk, causal, dtype)
     _check_sel(sel.cpu().numpy(), ref, "sel")
     ref_sc = np.take_along_axis(raw, ref, axis=-1)
@@ -93,21 +94,22 @@ def test_select_config3_full_size_sampled_rows():
     _check_sel(sel[:, rows], ref, "sel (sampled rows)")
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_select_quest_config4_shape(dtype):
+@pytest.mark.parametrize("dtype,engine", [("bf16", "auto"), ("bf16", "fp64"), ("f32", "auto")])
+def test_select_quest_config4_shape(dtype, engine):
     # config 4 selector: Hq16 Hkv2 D256 bs128 nblk512 top-32 + own + sink
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(3)
     B, Hq, Hkv, N, D, bs, topk = 1, 16, 2, 65536, 256, 128, 32
     q = randn(g, (B, Hq, N, D), dtype)
     k = randn(g, (B, Hkv, N, D), dtype)
-    _say("quest config 4", dtype)
-    idx = selection.select_quest(q.to(DEV), k.to(DEV), bs, topk, sink=True).cpu().numpy()
+    _say("quest config 4", dtype, engine)
+    idx = selection.select_quest(q.to(DEV), k.to(DEV), bs, topk, sink=True, engine=engine).cpu().numpy()
     ref, _ = osel.select_quest(np64(q), np64(k), bs, topk, True, dtype)
     _check_sel(idx, ref, "idx")
 
 
-def test_select_max2_module_scores():
+@pytest.mark.parametrize("engine", ["auto", "fp64"])
+def test_select_max2_module_scores(engine):
     # BlockSparseSSA._scores: max(sq . sk_mean, sq . sk_max) (src/ssa_model.py:113-119)
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(4)
@@ -118,7 +120,7 @@ def test_select_max2_module_scores():
     a = selection.pool(sq.to(DEV), bs, "mean_tok_then_grp")
     km = selection.pool(sk.to(DEV), bs, "mean_tok_then_grp")
     kx = selection.pool(sk.to(DEV), bs, "max")
-    sel, sc = selection.select(a, km, kx, score="max2", topk=topk, causal=True, need_scores=True)
+    sel, sc = selection.select(a, km, kx, score="max2", topk=topk, causal=True, need_scores=True, engine=engine)
     ra = osel.pool_tok(np64(sq)[:, 0], bs, "bf16", "mean")
     rkm = osel.pool_tok(np64(sk)[:, 0], bs, "bf16", "mean")
     rkx = osel.pool_tok(np64(sk)[:, 0], bs, "bf16", "max")
@@ -128,15 +130,18 @@ def test_select_max2_module_scores():
     assert np.array_equal(sc.cpu().numpy()[:, 0].astype(np.float64), np.take_along_axis(raw, ref, -1))
 
 
+@pytest.mark.parametrize("engine", ["auto", "fp64"])
 @pytest.mark.parametrize("nblk,topk,conv", [(1, 4, "own_first"), (3, 8, "own_first"), (5, 0, "own_first"),
-                                            (1, 4, "sorted_sink"), (4, 9, "sorted_sink"), (70, 62, "own_first")])
-def test_select_edge_budgets(nblk, topk, conv):
+                                            (1, 4, "sorted_sink"), (4, 9, "sorted_sink"), (70, 62, "own_first"),
+                                            (200, 62, "sorted_sink")])
+def test_select_edge_budgets(nblk, topk, conv, engine):
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(5)
     a = randn(g, (1, 2, nblk, 32), "bf16")
     b = randn(g, (1, 2, nblk, 32), "bf16")
     _say("edge", nblk, topk, conv)
-    sel = selection.select(a.to(DEV), b.to(DEV), topk=topk, convention=conv, sink=conv == "sorted_sink").cpu().numpy()
+    sel = selection.select(a.to(DEV), b.to(DEV), topk=topk, convention=conv, sink=conv == "sorted_sink",
+                           engine=engine).cpu().numpy()
     raw = osel.scores(np64(a), np64(b), "bf16", "dot")
     if conv == "own_first":
         ref = np.stack([osel.select_conv_a(raw[:, h], topk, True) for h in range(2)], 1)
@@ -145,12 +150,73 @@ def test_select_edge_budgets(nblk, topk, conv):
     _check_sel(sel, ref, "sel")
 
 
-def test_select_ties_break_to_lower_index():
+@pytest.mark.parametrize("D", [16, 64])
+def test_select_ties_break_to_lower_index(D):
     # all-equal scores: every candidate ties; lowest indices must win
     from fbsa_amd import selection
     nblk, topk = 200, 7
-    a = torch.ones(1, 1, nblk, 16, dtype=torch.bfloat16)
+    a = torch.ones(1, 1, nblk, D, dtype=torch.bfloat16)
     sel = selection.select(a.to(DEV), a.to(DEV), topk=topk, causal=True).cpu().numpy()[0, 0]
     for i in range(nblk):
         want = [i] + [j for j in range(min(i, topk))] + [i] * max(0, topk - i)
         assert sel[i].tolist() == want, (i, sel[i])
+
+
+def test_select_config5_prefix_invariance_and_sampled_rows():
+    # config 5: B1 H8 D64 N4194304 bs64 (nblk 65536) top-16. The streaming selection
+    # on the full sequence must give the 262144-token prefix run's blocks for the
+    # first 4096 rows (causal), and the oracle's blocks on sampled later rows.
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(5)
+    B, H, N, D, bs, topk = 1, 8, 4194304, 64, 64, 16
+    q = randn(g, (B, H, N, D), "bf16")
+    k = randn(g, (B, H, N, D), "bf16")
+    _say("config 5 selection")
+    qd, kd = q.to(DEV), k.to(DEV)
+    sel = selection.select_mean_pooled(qd, kd, bs, topk, True).cpu().numpy()
+    pre = selection.select_mean_pooled(qd[:, :, :262144].contiguous(), kd[:, :, :262144].contiguous(),
+                                       bs, topk, True).cpu().numpy()
+    _check_sel(sel[:, :4096], pre, "prefix rows")
+    qp = selection.pool(qd, bs, "mean_tok_then_grp", grp=H)[:, 0].float().cpu().numpy().astype(np.float64)
+    kp = selection.pool(kd, bs, "mean_tok_then_grp", grp=H)[:, 0].float().cpu().numpy().astype(np.float64)
+    rows = np.unique(np.concatenate([np.arange(65536 - 8, 65536),
+                                     np.random.default_rng(1).integers(4096, 65536, 40)]))
+    raw = osel.scores(qp, kp, "bf16", "dot", rows=rows)
+    ref = osel.select_conv_a(raw, topk, True, rows=rows)
+    _check_sel(sel[:, rows], ref, "sampled rows")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("score", ["dot", "max2", "quest"])
+@pytest.mark.parametrize("conv,causal,topk", [("own_first", True, 16), ("own_first", False, 16),
+                                              ("sorted_sink", True, 16), ("own_first", True, 48)])
+@pytest.mark.parametrize("ties,chunk", [(False, 0), (True, 0), (False, 4), (True, 1)])
+def test_select_tiled_modes(dtype, D, score, conv, causal, topk, ties, chunk):
+    # The MFMA engine over every score mode / convention / width it takes, with
+    # nblk = 700 (11 candidate tiles, a ragged last tile). chunk > 0 splits the
+    # candidates of a row block over several workgroups (partial lists + merge).
+    # ties=True uses small integer operands, so scores are exact integers with
+    # many exact ties (tie-break and exact-bracket paths).
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(6)
+    B, H, nblk = 1, 2, 700
+    if ties:
+        mk = lambda: torch.randint(-2, 3, (B, H, nblk, D), generator=g).to(getattr(torch, {"bf16": "bfloat16", "f16": "float16"}[dtype]))
+    else:
+        mk = lambda: randn(g, (B, H, nblk, D), dtype)
+    a, b1, b2 = mk(), mk(), mk()
+    if score == "quest":  # kmax >= kmin element-wise, as the pooled operands are
+        b1, b2 = torch.maximum(b1, b2), torch.minimum(b1, b2)
+    _say("tiled", dtype, D, score, conv, causal, topk, ties, chunk)
+    sink = conv == "sorted_sink"
+    sel, sc = selection.select(a.to(DEV), b1.to(DEV), b2.to(DEV) if score != "dot" else None, score=score,
+                               convention=conv, topk=topk, causal=causal, sink=sink, need_scores=True,
+                               chunk_tiles=chunk)
+    raw = osel.scores(np64(a), np64(b1), dtype, score, b2=np64(b2))
+    if conv == "own_first":
+        ref = np.stack([osel.select_conv_a(raw[:, h], topk, causal) for h in range(H)], 1)
+    else:
+        ref = osel.select_conv_b(raw, topk, sink)
+    _check_sel(sel.cpu().numpy(), ref, "sel")
+    assert np.array_equal(sc.cpu().numpy().astype(np.float64), np.take_along_axis(raw, ref, -1))
