@@ -16,6 +16,7 @@
 // ballot + shift. The four per-wave lists are merged in LDS at the end. The
 // nblk x nblk score matrix never exists in memory.
 #include <math.h>
+#include <type_traits>
 
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
@@ -840,8 +841,7 @@ template <typename T, int D, int MODE> struct SelTCfg {
   static constexpr int CAP = 64;                 // per-row key buffer
   static constexpr int NST = NOP * OPB <= 8192 ? 4 : 2;  // ring depth: about 74 KB of LDS, 2 workgroups per CU
   static constexpr int OFF_BUF = NST * STB;
-  static constexpr int OFF_QRAW = OFF_BUF + 64 * (CAP + 1) * 8;
-  static constexpr int OFF_ROWN = OFF_QRAW + 64 * D * 2;
+  static constexpr int OFF_ROWN = OFF_BUF + 64 * (CAP + 1) * 8;
   static constexpr int OFF_CNT = OFF_ROWN + 2 * 64 * 4;
   static constexpr int LDS = OFF_CNT + 64 * 4;
   static_assert(LPT * 256 * 16 == NOP * OPB, "stage must split evenly over threads");
@@ -866,6 +866,10 @@ __device__ __forceinline__ float pick4(float v0, float v1, float v2, float v3, i
   return (i & 2) ? hi : lo;
 }
 __device__ __forceinline__ float pick4(const float (&v)[4], int i) { return pick4(v[0], v[1], v[2], v[3], i); }
+__device__ __forceinline__ int pick4i(const int (&v)[4], int i) {
+  const int lo = (i & 1) ? v[1] : v[0], hi = (i & 1) ? v[3] : v[2];
+  return (i & 2) ? hi : lo;
+}
 __device__ __forceinline__ float pick16(const f32x4 (&v)[4], int t, int r) {
   return pick4(pick4(v[0][0], v[1][0], v[2][0], v[3][0], t), pick4(v[0][1], v[1][1], v[2][1], v[3][1], t),
                pick4(v[0][2], v[1][2], v[2][2], v[3][2], t), pick4(v[0][3], v[1][3], v[2][3], v[3][3], t), r);
@@ -938,8 +942,7 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   // before them, which would drain the prefetch ring.
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *ring = smem;                                             // NST stages
-  auto buf = (uint64_t(*)[C::CAP + 1])(smem + C::OFF_BUF);     // per-row key buffers (padded pitch)
-  auto qraw = (short(*)[D])(smem + C::OFF_QRAW);               // query rows (fp64 fallback)
+  auto buf = (uint64_t(*)[C::CAP + 1])(smem + C::OFF_BUF);     // per-row entry buffers (padded pitch)
   auto rown = (float(*)[64])(smem + C::OFF_ROWN);              // bf16_up(CB |a-part|) per row
   int *cnt = (int *)(smem + C::OFF_CNT);                       // key buffer fill
 
@@ -968,19 +971,14 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   const char *Nop[2] = {(const char *)(a.bn1 + bh * nbp), (const char *)(a.bn2 + bh * nbp)};
   const float *Anrm[2] = {a.an1 + bh * nbp, a.an2 + bh * nbp};
 
-  // query rows (16-bit patterns) for the exact fallback, per-row beta factors
-  // and counters; MFMA A fragments of this wave's 16 rows (lane p <-> row
-  // r0 + 16w + p) and the rank-1 fragments (k = 0 held by lanes g == 0)
-  for (int e = tid; e < 64 * D / 8; e += 256) {
-    const int r = e / (D / 8), c8 = e % (D / 8);
-    const int64_t i = r0 + r < a.nblk ? r0 + r : a.nblk - 1;
-    *(s16x8 *)&qraw[r][8 * c8] = *(const s16x8 *)(A + i * D + 8 * c8);
-  }
+  // per-row beta factors and counters; MFMA A fragments of this wave's 16
+  // rows (lane p <-> row r0 + 16w + p) and the rank-1 fragments (k = 0 held
+  // by lanes g == 0)
   if (tid < 64) cnt[tid] = 0;
   if (tid < 64 * NA) {
     const int r = tid & 63;
     const int64_t i = r0 + r < a.nblk ? r0 + r : a.nblk - 1;
-    rown[tid >> 6][r] = __uint_as_float(bf16_up_bits(CB * Anrm[tid >> 6][i]) << 16);
+    rown[tid >> 6][r] = __uint_as_float(bf16_up_bits(CB * (tid < 64 ? Anrm[0] : Anrm[1])[i]) << 16);
   }
   s16x8 af[NA][C::KS];
   s16x8 alo[NA], ahi[NA];
@@ -1046,13 +1044,37 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     }
   };
 
-  // Cuts row 16w + qq (wave-uniform) of the key buffer to its top K, in
-  // descending order, and raises the row's reject boundary.
+  // A buffered entry is either an exact key (make_key: low word ~j, bit 31
+  // set) or a pending candidate: low word j + 1 (nonzero, bit 31 clear), high
+  // word the bits of its MFMA upper bound (DOT, MAX2). resolve() turns a pending entry of row
+  // q into its exact key: the rounded bracket [hi - 2.02 beta, hi] when it
+  // pins the score, else the fp64 dot product from global memory.
+  auto resolve = [&](uint64_t e, int q) -> uint64_t {
+    if (e == 0 || ((uint32_t)e & 0x80000000u)) return e;
+    const int j = (int)(uint32_t)e - 1;
+    float sc = 0.f;
+    bool done = false;
+    if constexpr (MODE != FBSA_SCORE_QUEST) {
+      const float hi = __uint_as_float((uint32_t)(e >> 32));
+      float bj = a.bn1[bh * nbp + j];
+      if constexpr (MODE == FBSA_SCORE_MAX2) bj = fmaxf(bj, a.bn2[bh * nbp + j]);
+      const float beta = rown[0][q] * bj;
+      const float rl = round_dt_f<T>(hi - 2.02f * beta), rh = round_dt_f<T>(hi);
+      if (rl == rh && isfinite(rh)) {
+        sc = rh;
+        done = true;
+      }
+    }
+    if (!done) sc = exact_score_global<T, D, MODE>(a, bh, r0 + q, j);
+    return make_key(sc, j);
+  };
+
+  // Cuts row 16w + qq (wave-uniform) of the entry buffer to its top K exact
+  // keys, in descending order, and raises the row's reject boundary.
   float rej[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  auto compact = [&](int qq) {
+  auto compact = [&](int qq, int n) -> int {
     const int q = 16 * w + qq;
-    const int n = __builtin_amdgcn_readfirstlane(cnt[q]);
-    const uint64_t key = lane < n ? buf[q][lane] : 0;
+    const uint64_t key = lane < n ? resolve(buf[q][lane], q) : 0;
     // rank = number of larger keys (keys are distinct), from lane reads: no LDS round trips
     int rank = 0;
     for (int m = 0; m < n; ++m) rank += readlane_u64(key, m) > key ? 1 : 0;
@@ -1067,12 +1089,16 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
           if (r == (qq & 3)) rej[r] = fmaxf(rej[r], nb);
       }
     }
-    if (lane == 0) cnt[q] = n < K ? n : K;
     __builtin_amdgcn_s_waitcnt(0xC07F);
+    return n < K ? n : K;
   };
 
   // validity of (row 4g + r, candidate 16t + p) on a diagonal or ragged tile: bit 4t + r
   const int ilim = (int)(a.nblk - r0 < 64 ? a.nblk - r0 : 64);
+  uint32_t rowmask = 0;  // rows of this lane that exist (the last row block may be ragged)
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (16 * w + 4 * g + r < ilim) rowmask |= 0x1111u << r;
   auto valid_mask = [&](int64_t tl) {
     const int jlim = (int)(a.nblk - tl * 64 < 64 ? a.nblk - tl * 64 : 64);
     const bool diag = tl == rb;
@@ -1095,40 +1121,44 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) smax[t][r] = -INFINITY;
+  int rcl[4] = {0, 0, 0, 0};  // entries buffered for rows 16w + 4g + r (same in all lanes of a group)
 
-  // stage k of the ring holds tile t0 + k % nt of pass k / nt
-  auto tile_of = [&](int k) { return t0 + (k < nt ? k : k - nt); };
+  // Tile order within each pass: the full off-diagonal tiles first, then the
+  // (at most two) diagonal / ragged tiles, so those get loop bodies of their own.
+  const int64_t big = INT64_MAX / 4;
+  int64_t m1 = rb >= t0 && rb < t1 ? rb : big;                               // diagonal
+  int64_t m2 = (a.nblk & 63) && t1 == (a.nblk + 63) / 64 ? t1 - 1 : big;  // ragged last tile
+  if (m2 == m1) m2 = big;
+  if (m2 < m1) { const int64_t tmp = m1; m1 = m2; m2 = tmp; }
+  const int nm = (m1 != big) + (m2 != big);
+  const int nu = nt - nm;
+  auto tile_of = [&](int k) -> int64_t {  // stage k: tile of pass k / nt
+    const int kk = k < nt ? k : k - nt;
+    if (kk >= nu) return kk == nu ? m1 : m2;
+    int64_t u = t0 + kk;
+    if (u >= m1) ++u;
+    if (u >= m2) ++u;
+    return u;
+  };
+
 #pragma unroll
   for (int k = 0; k < NST - 1; ++k)
     if (k < 2 * nt) issue(tile_of(k), k);
-  for (int it = 0; it < 2 * nt; ++it) {
+
+  // one ring step: wait for stage it, refill, score its tile (lo in pass 1, hi in pass 2)
+  auto step = [&](int it, auto masked_c, auto collect_c) {
+    constexpr bool MASKED = decltype(masked_c)::value, COLLECT = decltype(collect_c)::value;
     const int stg = it % NST;
-    const bool collect = it >= nt;
     const int64_t tl = tile_of(it);
     // this wave's loads of stage it have landed (LPT + 1 per stage; later stages may be in flight)
     const int ahead = 2 * nt - 1 - it < NST - 2 ? 2 * nt - 1 - it : NST - 2;
     wait_ring<C::LPT + 1>(ahead);
     lds_barrier();  // every wave's part has landed; the stage refilled next is no longer read
     if (it + NST - 1 < 2 * nt) issue(tile_of(it + NST - 1), (it + NST - 1) % NST);
-    if (it == nt) {
-      // pass-1 bound: K-th largest of the row's 64 stream maxima
-      float v[4][4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) v[r][t] = smax[t][r];
-      group_sort64x4_desc(v, p);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float tau = __shfl(pick4(v[r], (K - 1) & 3), 16 * g + ((K - 1) >> 2), 64);
-        rej[r] = reject_boundary<T>(round_dt_f<T>(tau));
-      }
-    }
     const char *st = ring + stg * C::STB;
     const float *nrm = (const float *)(st + C::NOP * C::OPB);
     const int64_t j0 = tl * 64;
 
-    // lo (pass 1) or hi (pass 2) of the wave's 16 rows x 64 candidates
     s16x8 bfr[C::NOP][4][C::KS];
     s16x8 bp[C::NOP][4];
 #pragma unroll
@@ -1146,7 +1176,7 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
 #pragma unroll
     for (int op = 0; op < C::NOP; ++op) {
       const int oa = MODE == FBSA_SCORE_QUEST ? op : 0;
-      const s16x8 ar = collect ? ahi[oa] : alo[oa];
+      const s16x8 ar = COLLECT ? ahi[oa] : alo[oa];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         // rank-1 term (k = 0 of an extra bf16 k-block). For bf16 operands it
@@ -1154,17 +1184,16 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
         // product added afterwards (a chain mixing MFMA opcodes through the
         // accumulator reads it before the first product has landed)
         const f32x4 r1 = Mfma16<bf16>::run(ar, bp[op][t], f32x4{0.f, 0.f, 0.f, 0.f});
-        acc[op][t] = sizeof(T) == 2 && __is_same(T, bf16) ? r1 : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[op][t] = __is_same(T, bf16) ? r1 : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) acc[op][t] = Mfma16<T>::run(af[oa][ks], bfr[op][t][ks], acc[op][t]);
         if constexpr (!__is_same(T, bf16)) acc[op][t] += r1;
       }
     }
-    const bool masked = tl == rb || j0 + 64 > a.nblk;  // diagonal or ragged tile
+    const uint32_t vm = MASKED ? valid_mask(tl) : rowmask;
 
-    if (!collect) {
+    if constexpr (!COLLECT) {
       // pass 1: stream maxima of the lower ends (a NaN end is ignored)
-      const uint32_t vm = masked ? valid_mask(tl) : 0xFFFFu;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1172,89 +1201,107 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
           float lo0 = acc[0][t][r], lo1 = -INFINITY;
           if constexpr (MODE == FBSA_SCORE_QUEST) lo0 = round_dt_f<T>(acc[0][t][r]) + round_dt_f<T>(acc[1][t][r]);
           if constexpr (MODE == FBSA_SCORE_MAX2) lo1 = acc[1][t][r];
-          if (masked && !((vm >> (4 * t + r)) & 1u)) lo0 = lo1 = -INFINITY;
+          if (MASKED && !((vm >> (4 * t + r)) & 1u)) lo0 = lo1 = -INFINITY;
           smax[t][r] = vmax(smax[t][r], lo0);
           if constexpr (MODE == FBSA_SCORE_MAX2) smax[t][r] = vmax(smax[t][r], lo1);
         }
-      continue;
-    }
-
-    // pass 2: reject against the row's boundary (NaN survives)
-    bool s[4][4];
-    uint64_t any = 0;
+      return;
+    } else {
+      // pass 2: reject against the row's boundary (NaN survives)
+      bool sr[4][4];
+      uint64_t any = 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (MODE == FBSA_SCORE_QUEST) {
-          s[t][r] = !(round_dt_f<T>(acc[0][t][r]) + round_dt_f<T>(acc[1][t][r]) < rej[r]);
-        } else {
-          s[t][r] = !(acc[0][t][r] < rej[r]);
-          if constexpr (MODE == FBSA_SCORE_MAX2) s[t][r] = s[t][r] || !(acc[1][t][r] < rej[r]);
-        }
-        any |= __ballot(s[t][r]);
-      }
-    if (!any) continue;
-    const uint32_t vm = masked ? valid_mask(tl) : 0xFFFFu;
-    uint32_t sv = 0;  // bit 4t + r: candidate 16t + p survives for row 4g + r
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sv |= s[t][r] ? 1u << (4 * t + r) : 0u;
-    sv &= vm;
-
-    // survivors: one per lane per round, exact keys appended to the row buffers
-    while (__ballot(sv != 0)) {
-      {  // a round adds at most 16 keys to a row (one per lane of its group)
-        const int c = lane < 16 ? cnt[16 * w + lane] : 0;
-        uint64_t ov = __ballot(lane < 16 && c > C::CAP - 16);
-        while (ov) {
-          const int qq = (int)__builtin_ctzll(ov);
-          ov &= ov - 1;
-          compact(qq);
-        }
-      }
-      const bool has = sv != 0;
-      const int b = has ? __builtin_ctz(sv) : 0;
-      sv &= sv - 1;
-      if (has) {
-        const int t = b >> 2, r = b & 3;
-        const int q = 16 * w + 4 * g + r;
-        const int row = 16 * t + p;
-        float ex[2] = {0.f, 0.f};
-#pragma unroll
-        for (int op = 0; op < C::NOP; ++op) {
-          const float hi = pick16(acc[op], t, r);
-          // (beta factors from LDS: indexing the register copies by t, r would spill)
-          const float beta = rown[MODE == FBSA_SCORE_QUEST ? op : 0][q] * nrm[(t * C::NOP + op) * 16 + p];
-          const float rl = round_dt_f<T>(hi - 2.02f * beta), rh = round_dt_f<T>(hi);
-          if (rl == rh && isfinite(rh)) {
-            ex[op] = rh;
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (MODE == FBSA_SCORE_QUEST) {
+            sr[t][r] = !(round_dt_f<T>(acc[0][t][r]) + round_dt_f<T>(acc[1][t][r]) < rej[r]);
           } else {
-            // exact fp64 dot product from the staged candidate row and the query row
-            double d = 0.0;
-            for (int c = 0; c < C::CPR; ++c) {
-              const s16x8 bv = *(const s16x8 *)(st + op * C::OPB + (row * C::CPR + (c ^ swz(row, C::CPR))) * 16);
+            sr[t][r] = !(acc[0][t][r] < rej[r]);
+            if constexpr (MODE == FBSA_SCORE_MAX2) sr[t][r] = sr[t][r] || !(acc[1][t][r] < rej[r]);
+          }
+          any |= __ballot(sr[t][r]);
+        }
+      if (!any) return;
+      uint32_t sv = 0;  // bit 4t + r: candidate 16t + p survives for row 4g + r
 #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                double av = (double)half_bits_to_f32<T>((uint32_t)(unsigned short)qraw[q][8 * c + e]);
-                if (MODE == FBSA_SCORE_QUEST) av = op == 0 ? (av > 0.0 ? av : 0.0) : (av < 0.0 ? av : 0.0);
-                d = __builtin_fma(av, (double)half_bits_to_f32<T>((uint32_t)(unsigned short)bv[e]), d);
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv |= sr[t][r] ? 1u << (4 * t + r) : 0u;
+      sv &= vm;
+
+      // survivors, one per lane per round, appended as pending entries; the
+      // slots come from ballots (rows of a group only receive entries from
+      // that group's 16 lanes), the counts live in registers
+      const uint64_t gm = 0xFFFFull << (16 * g);
+      while (__ballot(sv != 0)) {
+        {  // a round adds at most 16 entries to a row
+          const bool near = rcl[0] > C::CAP - 16 || rcl[1] > C::CAP - 16 || rcl[2] > C::CAP - 16 || rcl[3] > C::CAP - 16;
+          uint64_t ov = __ballot(near && p == 0);
+          while (ov) {
+            const int gg = (int)__builtin_ctzll(ov) >> 4;
+            ov &= ov - 1;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const int n = __builtin_amdgcn_readlane(rcl[rr], 16 * gg);
+              if (n > C::CAP - 16) {
+                const int nn = compact(4 * gg + rr, n);
+                if (g == gg) rcl[rr] = nn;
               }
             }
-            ex[op] = round_dt<T>(d);
           }
         }
-        float sc;
-        if constexpr (MODE == FBSA_SCORE_DOT) sc = ex[0];
-        else if constexpr (MODE == FBSA_SCORE_MAX2) sc = fmaxf(ex[0], ex[1]);
-        else sc = round_dt_f<T>(ex[0] + ex[1]);
-        const int slot = lds_fetch_add(&cnt[q], 1);
-        buf[q][slot] = make_key(sc, (int)(j0 + row));
+        const bool has = sv != 0;
+        const int b = has ? __builtin_ctz(sv) : 0;
+        sv &= sv - 1;
+        const int t = b >> 2, r = b & 3;
+        uint64_t mr[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) mr[rr] = __ballot(has && r == rr);
+        if (has) {
+          const uint64_t mine = (r == 0 ? mr[0] : r == 1 ? mr[1] : r == 2 ? mr[2] : mr[3]) & gm;
+          const int off = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mine >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mine, 0u));
+          uint32_t hb = 0;
+          if constexpr (MODE == FBSA_SCORE_DOT) {
+            hb = __float_as_uint(pick16(acc[0], t, r));
+          } else if constexpr (MODE == FBSA_SCORE_MAX2) {
+            const float h0 = pick16(acc[0], t, r), h1 = pick16(acc[1], t, r);
+            hb = __float_as_uint(h0 != h0 || h1 != h1 ? __builtin_nanf("") : fmaxf(h0, h1));
+          }
+          buf[16 * w + 4 * g + r][pick4i(rcl, r) + off] = ((uint64_t)hb << 32) | (uint32_t)(j0 + 16 * t + p + 1);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) rcl[rr] += __popcll(mr[rr] & gm);
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);
+    }
+  };
+
+  using F = std::integral_constant<bool, false>;
+  using Tr = std::integral_constant<bool, true>;
+  for (int it = 0; it < nu; ++it) step(it, F{}, F{});
+  for (int it = nu; it < nt; ++it) step(it, Tr{}, F{});
+  {
+    // pass-1 bound: K-th largest of the row's 64 stream maxima
+    float v[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[r][t] = smax[t][r];
+    group_sort64x4_desc(v, p);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float tau = __shfl(pick4(v[r], (K - 1) & 3), 16 * g + ((K - 1) >> 2), 64);
+      rej[r] = reject_boundary<T>(round_dt_f<T>(tau));
     }
   }
+  for (int it = nt; it < nt + nu; ++it) step(it, F{}, Tr{});
+  for (int it = nt + nu; it < 2 * nt; ++it) step(it, Tr{}, Tr{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  if (p == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cnt[16 * w + 4 * g + r] = rcl[r];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
 
   // this chunk's top K of each row, 4 rows at a time (one per lane group):
   // lane p ranks keys p, p + 16, p + 32, p + 48 of its row against the row's
@@ -1266,6 +1313,10 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     const int nmax = __builtin_amdgcn_readfirstlane(
         max(max(__builtin_amdgcn_readlane(n, 0), __builtin_amdgcn_readlane(n, 16)),
             max(__builtin_amdgcn_readlane(n, 32), __builtin_amdgcn_readlane(n, 48))));
+    // pending entries -> exact keys, in place (one resolve() instance: the loop stays rolled)
+#pragma unroll 1
+    for (int e = p; e < n; e += 16) buf[q][e] = resolve(buf[q][e], q);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     uint64_t k[4];
     int rk[4];
 #pragma unroll
@@ -1273,10 +1324,14 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
       k[e] = p + 16 * e < n ? buf[q][p + 16 * e] : 0;
       rk[e] = 0;
     }
-    for (int m = 0; m < nmax; ++m) {
-      const uint64_t km = m < n ? buf[q][m] : 0;
+    for (int m = 0; m < nmax; m += 4) {
+      uint64_t km[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) rk[e] += km > k[e] ? 1 : 0;
+      for (int u = 0; u < 4; ++u) km[u] = m + u < n ? buf[q][m + u] : 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rk[e] += km[u] > k[e] ? 1 : 0;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
