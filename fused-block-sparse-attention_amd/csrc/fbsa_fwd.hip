@@ -74,8 +74,10 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   __shared__ int s_nvalid;
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, p = lane & 15;
-  const int64_t total = a.B * a.Hq * a.nblk;
-  int64_t t = a.order ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, total);
+  // launch order: consecutive workgroups are the query heads of one KV group,
+  // then consecutive query blocks (round-robin over the XCDs measured faster
+  // for the gathered K/V than XCD-contiguous ranges)
+  int64_t t = blockIdx.x;
   const int hin = (int)(t % a.grp); t /= a.grp;
   const int64_t i = t % a.nblk; t /= a.nblk;
   const int hk = (int)(t % a.Hkv);
@@ -433,24 +435,7 @@ static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
   return hip_check(hipGetLastError(), "fwd_kernel launch");
 }
 
-static int fwd_variant() {
-  static const int v = [] {
-    const char *e = getenv("FBSA_FWD_CFG");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
 template <typename T, int BS> static int dispatch_d(const FwdArgs &a, int64_t D, hipStream_t s) {
-  if constexpr (sizeof(T) == 2 && BS == 64) {
-    if (D == 64) switch (fwd_variant()) {
-      case 1: return launch_fwd<T, BS, 64, 1, 64, 3>(a, s);
-      case 2: return launch_fwd<T, BS, 64, 2>(a, s);
-      case 3: return launch_fwd<T, BS, 64, 2, 64, 3>(a, s);
-      case 4: return launch_fwd<T, BS, 64, 4>(a, s);
-      case 5: return launch_fwd<T, BS, 64, 2, 32, 4>(a, s);
-    }
-  }
   switch (D) {
     case 32: return launch_fwd<T, BS, 32>(a, s);
     case 64: return launch_fwd<T, BS, 64>(a, s);
@@ -470,13 +455,7 @@ template <typename T> static int dispatch_bs(const FwdArgs &a, int64_t bs, int64
   return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: block size %lld not in {16,32,64,128}", (long long)bs);
 }
 
-int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a0, hipStream_t s) {
-  static const int order = [] {
-    const char *e = getenv("FBSA_FWD_ORDER");
-    return e ? atoi(e) : 0;
-  }();
-  FwdArgs a = a0;
-  a.order = order;
+int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s) {
   switch (d->dtype) {
     case FBSA_BF16: return dispatch_bs<bf16>(a, d->bs, d->D, s);
     case FBSA_F16: return dispatch_bs<f16>(a, d->bs, d->D, s);

@@ -20,7 +20,6 @@ struct FwdArgs {
   float scale2;  // softmax scale * log2(e)
   int mask;
   int grp;
-  int order;  // workgroup -> (b, head, block) order: 0 XCD-contiguous, 1 launch order
 };
 
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
