@@ -88,6 +88,25 @@ def test_select_rejects_bad_budget():
     assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EUNSUPPORTED
 
 
+def test_select_flags_and_workspace_size():
+    lib = _lib.load()
+    d = _lib.SelectDesc()
+    d.dtype, d.score, d.convention, d.causal = _lib.BF16, _lib.SCORE_DOT, _lib.SEL_OWN_FIRST, 1
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = 1, 8, 4096, 64, 16, 17
+    d.flags = 1  # only the chunk field (bits 8..23) is defined
+    assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EINVAL
+    assert "flags" in lib.fbsa_last_error().decode()
+    # MFMA engine workspace: 4 padded norm arrays + per-(row, chunk) partial top-k lists
+    d.flags = 0
+    auto = lib.fbsa_select_workspace_bytes(d)
+    npad = 8 * 4096
+    assert auto >= 4 * npad * 4
+    d.flags = 4 << _lib.SEL_CHUNK_SHIFT   # 16 chunks of 4 tiles: larger partial-list area
+    assert lib.fbsa_select_workspace_bytes(d) == 4 * npad * 4 + 256 + 8 * 4096 * 16 * 16 * 8
+    d.dtype = _lib.F32   # fp32 operands take the fp64 engine: no workspace
+    assert lib.fbsa_select_workspace_bytes(d) == 0
+
+
 def test_python_ops_require_gpu_tensors():
     import torch
     from fbsa_amd import ops
