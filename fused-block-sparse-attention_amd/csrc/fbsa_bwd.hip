@@ -370,10 +370,12 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     if (c < nchunks) issue(c);
 
   for (int c = 0; c < nchunks; ++c) {
-    if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+    // stage c has landed for this wave (up to NSTAGE - 2 later stages may be in flight);
+    // after the barrier every wave is also done with chunk c - 1, whose stage is refilled
     const int ahead = nchunks - 1 - c;
-    wait_ring<C::LPT>(ahead < C::NSTAGE - 1 ? ahead : C::NSTAGE - 1);
+    wait_ring<C::LPT>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
     lds_barrier();
+    if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
 
     const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
     const char *Vs = Ks + C::TILE_BYTES;
@@ -411,7 +413,6 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
       dgl = 0.f;
     }
     mm_tr_acc<T, D, C::KC>(Ks, ds, dqacc, g, p);  // dQ^T += K^T dS^T
-    lds_barrier();
   }
 
   T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
@@ -508,10 +509,13 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
       if (c < nchunks) issue(c);
 
     for (int c = 0; c < nchunks; ++c) {
-      if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+      // stage c has landed for this wave (LPT + 1 loads per stage; up to NSTAGE - 2 later
+      // stages may still be in flight); after the barrier every wave's part has landed and
+      // every wave is done with chunk c - 1, whose stage the refill below overwrites
       const int ahead = nchunks - 1 - c;
-      wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 1 ? ahead : C::NSTAGE - 1);
+      wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
       lds_barrier();
+      if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
 
       const char *Qs = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
       const char *Ds = Qs + C::TILE_BYTES;
@@ -549,7 +553,6 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
         }
       mm_tr_acc<T, D, C::KC>(Ds, pp, dvacc, g, p);  // dV^T += dO^T P
       mm_tr_acc<T, D, C::KC>(Qs, ds, dkacc, g, p);  // dK^T += Q^T dS
-      lds_barrier();
     }
   }
 
