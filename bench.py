@@ -4,14 +4,19 @@ Workload (the north-star shape): bf16, B=1, H=8,
 D=64, N=262144, block 64 (nblk=4096), causal, top-16 content blocks by
 mean-pooled q.k scores (kk=17), q,k,v ~ N(0,1)/sqrt(D). One step = pool q,
 pool k, streaming top-k selection, fused forward (plus the backward when
---bwd is given), all on device-resident inputs.
+--bwd is given), all on device-resident inputs, one after the other on one
+stream. ``--overlap`` times ``fbsa_amd.pipeline.select_and_attend`` instead,
+which overlaps the selection of later query blocks with the forward of
+earlier ones on a second stream (identical results; slower on MI355X at this
+shape, the two kernels contend for the CUs).
 
 Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step;
 ``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
 FLOP per launch, the reference's own formula, src/bench_crossover.py:105)
-timed with HIP events on the launch stream; ``cpu_baseline`` times the CPU
-oracle (numpy restatement of the reference gather path) on a bounded sample
-of query blocks and scales it to the whole workload.
+timed with HIP events on the launch stream in separate, unoverlapped
+launches; ``cpu_baseline`` times the CPU oracle (numpy restatement of the
+reference gather path) on a bounded sample of query blocks and scales it to
+the whole workload.
 """
 import argparse
 import json
@@ -40,6 +45,9 @@ def parse():
     p.add_argument("--bs", type=int, default=64)
     p.add_argument("--topk", type=int, default=16)
     p.add_argument("--bwd", action="store_true", help="also time the backward (separate fields)")
+    p.add_argument("--overlap", action="store_true",
+                   help="time the two-stream step (selection overlapped with the forward)")
+    p.add_argument("--splits", type=int, default=4, help="row ranges of the overlapped step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-rows", type=int, default=128, help="query blocks in the CPU sample")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -116,7 +124,7 @@ def main():
         calibrate_copy()
         return
     import torch
-    from fbsa_amd import ops, selection
+    from fbsa_amd import ops, pipeline, selection
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -132,7 +140,7 @@ def main():
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     fwd_ms, sel_ms = [], []
 
-    def step(timed):
+    def seq_step(timed):
         e0, e1, e2 = ev(), ev(), ev()
         e0.record(stream)
         sel = selection.select_mean_pooled(q, k, bs, topk, causal=True)
@@ -144,15 +152,26 @@ def main():
             fwd_ms.append((e1, e2))
         return sel, o, lse
 
+    def step():
+        if not a.overlap:
+            return seq_step(False)
+        return pipeline.select_and_attend(q, k, v, bs, topk, need_lse=True, splits=a.splits)
+
     for _ in range(a.warmup):
-        step(False)
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(a.steps):
-        step(True)
+        step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / a.steps
+    # unoverlapped launches for the per-stage times and the forward's roofline
+    for _ in range(a.warmup):
+        seq_step(False)
+    for _ in range(a.steps):
+        seq_step(True)
+    torch.cuda.synchronize()
     t_sel = sum(x.elapsed_time(y) for x, y in sel_ms) / a.steps
     t_fwd = sum(x.elapsed_time(y) for x, y in fwd_ms) / a.steps
 
@@ -170,7 +189,9 @@ def main():
         "dtype": "bf16", "data": "synthetic (q,k,v ~ N(0,1)/sqrt(D), seed 0, device generator)",
         "config": {"workload": "BASELINE configs[2]: block-pair selection (mean-pooled q.k, top-16, "
                                "own-first) + fused block-sparse forward, causal",
-                   "B": B, "H": H, "N": N, "D": D, "block": bs, "nblk": nblk, "topk": topk, "kk": kk},
+                   "B": B, "H": H, "N": N, "D": D, "block": bs, "nblk": nblk, "topk": topk, "kk": kk,
+                   "step": (f"selection overlapped with the forward ({a.splits} row ranges, 2 streams)" if a.overlap
+                            else "pool, select, forward in sequence on one stream")},
         "ms_select": t_sel, "ms_fwd": t_fwd,
         "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
@@ -187,7 +208,7 @@ def main():
     if a.bwd:
         from fbsa_amd import autograd  # noqa: F401
         bwd_ev = []
-        sel, o, lse = step(False)
+        sel, o, lse = seq_step(False)
         for it in range(a.warmup + a.steps):
             e0, e1 = ev(), ev()
             e0.record(stream)

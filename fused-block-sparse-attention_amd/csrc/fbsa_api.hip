@@ -81,8 +81,18 @@ int fbsa_version(void) { return 1; }
 
 int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const int32_t *sel,
              const float *gate, const void *out_gate, void *o, float *lse, void *stream) {
+  if (!d) return fail(FBSA_EINVAL, "fbsa_fwd: null descriptor");
+  return fbsa_fwd_rows(d, 0, d->nblk, q, k, v, sel, gate, out_gate, o, lse, stream);
+}
+
+int fbsa_fwd_rows(const fbsa_attn_desc *d, int64_t i_begin, int64_t i_end, const void *q, const void *k,
+                  const void *v, const int32_t *sel, const float *gate, const void *out_gate, void *o, float *lse,
+                  void *stream) {
   int e = check_attn(d, "fbsa_fwd");
   if (e) return e;
+  if (i_begin < 0 || i_end < i_begin || i_end > d->nblk)
+    return fail(FBSA_EINVAL, "fbsa_fwd: query-block range [%lld, %lld) outside [0, %lld)", (long long)i_begin,
+                (long long)i_end, (long long)d->nblk);
   if (!q || !k || !v || !sel || !o) return fail(FBSA_EINVAL, "fbsa_fwd: null tensor pointer");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
     return fail(FBSA_EINVAL, "fbsa_fwd: q/k/v/o must be 16-byte aligned");
@@ -92,6 +102,8 @@ int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
     return fail(FBSA_EINVAL, "fbsa_fwd: out_gate misaligned");
   FwdArgs a;
   fill_fwd(d, a);
+  a.i0 = i_begin;
+  a.ni = i_end - i_begin;
   a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse; a.sel = sel; a.gate = gate; a.og = out_gate;
   return run_fwd(d, a, (hipStream_t)stream);
 }
@@ -121,6 +133,16 @@ size_t fbsa_select_workspace_bytes(const fbsa_select_desc *d) { return d ? selec
 int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
                 float *sel_score, void *workspace, size_t workspace_bytes, void *stream) {
   if (!d) return fail(FBSA_EINVAL, "fbsa_select: null descriptor");
+  return fbsa_select_rows(d, 0, d->nblk, a, b1, b2, sel, sel_score, workspace, workspace_bytes, stream);
+}
+
+int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a, const void *b1,
+                     const void *b2, int32_t *sel, float *sel_score, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+  if (!d) return fail(FBSA_EINVAL, "fbsa_select: null descriptor");
+  if (row_begin < 0 || row_end < row_begin || row_end > d->nblk)
+    return fail(FBSA_EINVAL, "fbsa_select: row range [%lld, %lld) outside [0, %lld)", (long long)row_begin,
+                (long long)row_end, (long long)d->nblk);
   if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_select: bad dtype %d", d->dtype);
   if (d->score < FBSA_SCORE_DOT || d->score > FBSA_SCORE_QUEST) return fail(FBSA_EINVAL, "fbsa_select: bad score %d", d->score);
   if (d->convention != FBSA_SEL_OWN_FIRST && d->convention != FBSA_SEL_SORTED_SINK)
@@ -142,7 +164,7 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
   const size_t need = select_workspace_bytes(d);
   void *ws = (workspace && workspace_bytes >= need && need > 0) ? workspace : nullptr;
   if (ws && !aligned(ws, 16)) return fail(FBSA_EINVAL, "fbsa_select: workspace must be 16-byte aligned");
-  return run_select(d, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
+  return run_select(d, row_begin, row_end, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

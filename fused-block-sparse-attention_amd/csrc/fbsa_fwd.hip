@@ -79,7 +79,7 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   // for the gathered K/V than XCD-contiguous ranges)
   int64_t t = blockIdx.x;
   const int hin = (int)(t % a.grp); t /= a.grp;
-  const int64_t i = t % a.nblk; t /= a.nblk;
+  const int64_t i = a.i0 + t % a.ni; t /= a.ni;
   const int hk = (int)(t % a.Hkv);
   const int64_t b = t / a.Hkv;
   const int hq = hk * a.grp + hin;
@@ -430,7 +430,8 @@ static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
       attr_bytes = lds;
     }
   }
-  const int64_t nwg = a.B * a.Hq * a.nblk;
+  const int64_t nwg = a.B * a.Hq * a.ni;
+  if (nwg == 0) return FBSA_OK;
   hipLaunchKernelGGL((fwd_kernel<T, BS, D, QT, KCO, NSO>), dim3((unsigned)nwg), dim3(C::NT), lds, stream, a);
   return hip_check(hipGetLastError(), "fwd_kernel launch");
 }

@@ -16,6 +16,7 @@ struct FwdArgs {
   const float *gate;
   const void *og;
   int64_t B, Hq, Hkv, L, nblk, kk, hsel, l_valid;
+  int64_t i0, ni;  // query blocks [i0, i0 + ni) of this launch
   int64_t sq[3], sk[3], sv[3], so[3], sog[3];
   float scale2;  // softmax scale * log2(e)
   int mask;
@@ -25,8 +26,8 @@ struct FwdArgs {
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
 size_t select_workspace_bytes(const fbsa_select_desc *d);
-int run_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
-               float *sel_score, void *ws, hipStream_t s);
+int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *a, const void *b1, const void *b2,
+               int32_t *sel, float *sel_score, void *ws, hipStream_t s);
 
 // ---- backward ----
 // Byte offsets of the backward workspace regions (each 256-byte aligned).

@@ -451,6 +451,7 @@ struct SelArgs {
   uint64_t *part;                      // MFMA path: per-(row, candidate chunk) top-k keys
   int64_t B, H, nblk, D, topk, kk;
   int64_t ct, nch;                     // MFMA path: candidate tiles per chunk, chunks per row block
+  int64_t row0, row1;                  // query blocks (rows) selected by this launch
   int conv, causal, sink, score;
 };
 
@@ -502,11 +503,11 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
   __shared__ uint64_t lists[4][R][64];  // per-wave lists for the final merge
   __shared__ float diag[R], sinks[R];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int64_t ntile = (a.nblk + R - 1) / R;
+  const int64_t ntile = (a.row1 - a.row0 + R - 1) / R;
   // heavy (late) row tiles first: blockIdx 0 gets the last tile
   const int64_t t = ntile - 1 - (int64_t)blockIdx.x % ntile;
   const int64_t bh = blockIdx.x / ntile;  // b * H + h
-  const int64_t i0 = t * R;
+  const int64_t i0 = a.row0 + t * R;
   const T *A = (const T *)a.a + bh * a.nblk * D;
   const T *B1 = (const T *)a.b1 + bh * a.nblk * D;
   const T *B2 = MODE != FBSA_SCORE_DOT ? (const T *)a.b2 + bh * a.nblk * D : nullptr;
@@ -586,7 +587,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
   __syncthreads();
   for (int r = w; r < R; r += 4) {
     const int64_t i = i0 + r;
-    if (i >= a.nblk) continue;
+    if (i >= a.row1) continue;
     uint64_t mine = lists[0][r][lane];
     for (int ww = 1; ww < 4; ++ww)
       for (int l = 0; l < K; ++l) {
@@ -673,11 +674,13 @@ __device__ __forceinline__ float vmax(float m, float x) {
 __host__ __device__ static inline int64_t sel_norm_pitch(int64_t nblk) { return (nblk + 63) & ~(int64_t)63; }
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(256) void sel_norms_kernel(SelArgs a, float *an1, float *an2, float *bn1, float *bn2) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t n = a.B * a.H * a.nblk;
-  if (row >= n) return;
-  const int64_t nrow = row / a.nblk * sel_norm_pitch(a.nblk) + row % a.nblk;
+__global__ __launch_bounds__(256) void sel_norms_kernel(SelArgs a, int64_t nneed, float *an1, float *an2,
+                                                        float *bn1, float *bn2) {
+  // rows [0, nneed) of every (batch, head)
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= a.B * a.H * nneed) return;
+  const int64_t row = r / nneed * a.nblk + r % nneed;
+  const int64_t nrow = r / nneed * sel_norm_pitch(a.nblk) + r % nneed;
   const T *A = (const T *)a.a + row * D;
   const T *B1 = (const T *)a.b1 + row * D;
   const T *B2 = MODE != FBSA_SCORE_DOT ? (const T *)a.b2 + row * D : nullptr;
@@ -947,12 +950,13 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   int *cnt = (int *)(smem + C::OFF_CNT);                       // key buffer fill
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, p = lane & 15;
-  const int64_t nrb = (a.nblk + 63) / 64;
+  // row blocks [rb0, rb1) cover this launch's rows [row0, row1)
+  const int64_t rb0 = a.row0 / 64, rb1 = (a.row1 + 63) / 64, nrr = rb1 - rb0;
   // consecutive work items (same head) on one XCD, so its L2 holds that head's candidates
   int64_t x = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t ch = x % a.nch; x /= a.nch;
-  const int64_t rb = nrb - 1 - x % nrb;  // heavy (late) row blocks first
-  const int64_t bh = x / nrb;
+  const int64_t rb = rb1 - 1 - x % nrr;  // heavy (late) row blocks first
+  const int64_t bh = x / nrr;
   const int64_t r0 = rb * 64;
   const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
   const int64_t last_row = r0 + 63 < a.nblk - 1 ? r0 + 63 : a.nblk - 1;
@@ -1343,7 +1347,8 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   for (int qq = 0; qq < 16; ++qq) {
     const int q = 16 * w + qq;
     const int64_t i = r0 + q;
-    if (i >= a.nblk) break;
+    if (i >= a.row1) break;
+    if (i < a.row0) continue;
     const int n = __builtin_amdgcn_readfirstlane(cnt[q]);
     const uint64_t v = lane < n ? buf[q][lane] : 0;
     if (single) emit_row<T, D, MODE>(a, bh, i, v, lane, K);
@@ -1355,9 +1360,11 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256) void select_merge_kernel(SelArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (bh, i)
-  if (row >= a.B * a.H * a.nblk) return;
-  const int64_t i = row % a.nblk, bh = row / a.nblk;
+  const int64_t nr = a.row1 - a.row0;
+  const int64_t rr = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (bh, i - row0)
+  if (rr >= a.B * a.H * nr) return;
+  const int64_t i = a.row0 + rr % nr, bh = rr / nr;
+  const int64_t row = bh * a.nblk + i;
   const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
   const int64_t jmax = (a.causal || !convA) ? ((i / 64) * 64 + 63 < a.nblk - 1 ? (i / 64) * 64 + 63 : a.nblk - 1)
                                             : a.nblk - 1;
@@ -1401,30 +1408,36 @@ template <typename T, int D, int MODE> static bool sel_tiled_ok(const SelArgs &a
 }
 
 template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, void *ws, hipStream_t s) {
+  if (a.row1 <= a.row0) return FBSA_OK;
   if (ws && sel_tiled_ok<T, D, MODE>(a)) {
     if constexpr (sizeof(T) == 2 && (D == 32 || D == 64)) {
-      const int64_t n = a.B * a.H * a.nblk;
+      // norms of rows [0, nneed): the query rows' row blocks and every candidate they may select
+      const int64_t rb1 = (a.row1 + 63) / 64;
+      const int64_t nneed = (a.causal || a.conv != FBSA_SEL_OWN_FIRST) ? (rb1 * 64 < a.nblk ? rb1 * 64 : a.nblk)
+                                                                        : a.nblk;
+      const int64_t n = a.B * a.H * nneed;
       const int64_t npad = a.B * a.H * sel_norm_pitch(a.nblk);
       float *an1 = (float *)ws, *an2 = an1 + npad, *bn1 = an2 + npad, *bn2 = bn1 + npad;
-      hipLaunchKernelGGL((sel_norms_kernel<T, D, MODE>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, an1,
-                         an2, bn1, bn2);
+      hipLaunchKernelGGL((sel_norms_kernel<T, D, MODE>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a,
+                         nneed, an1, an2, bn1, bn2);
       int e = hip_check(hipGetLastError(), "sel_norms_kernel launch");
       if (e) return e;
       SelArgs b = a;
       b.an1 = an1; b.an2 = an2; b.bn1 = bn1; b.bn2 = bn2;
       b.part = (uint64_t *)(((uintptr_t)(bn2 + npad) + 255) & ~(uintptr_t)255);
-      const int64_t nrb = (a.nblk + 63) / 64;
+      const int64_t nrr = rb1 - a.row0 / 64;
       using C = SelTCfg<T, D, MODE>;
-      hipLaunchKernelGGL((select_tiled_kernel<T, D, MODE>), dim3((unsigned)(a.B * a.H * nrb * b.nch)), dim3(256),
+      hipLaunchKernelGGL((select_tiled_kernel<T, D, MODE>), dim3((unsigned)(a.B * a.H * nrr * b.nch)), dim3(256),
                          C::LDS, s, b);
       e = hip_check(hipGetLastError(), "select_tiled_kernel launch");
       if (e || b.nch == 1) return e;
-      hipLaunchKernelGGL((select_merge_kernel<T, D, MODE>), dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, b);
+      const int64_t nrows = a.B * a.H * (a.row1 - a.row0);
+      hipLaunchKernelGGL((select_merge_kernel<T, D, MODE>), dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, b);
       return hip_check(hipGetLastError(), "select_merge_kernel launch");
     }
   }
   constexpr int R = 8;
-  const int64_t ntile = (a.nblk + R - 1) / R;
+  const int64_t ntile = (a.row1 - a.row0 + R - 1) / R;
   const int64_t nwg = ntile * a.B * a.H;
   hipLaunchKernelGGL((select_kernel<T, D, R, MODE>), dim3((unsigned)nwg), dim3(256), 0, s, a);
   return hip_check(hipGetLastError(), "select_kernel launch");
@@ -1459,12 +1472,14 @@ size_t select_workspace_bytes(const fbsa_select_desc *d) {
          (size_t)(n * nch * (K > 0 ? K : 1)) * sizeof(uint64_t);
 }
 
-int run_select(const fbsa_select_desc *d, const void *av, const void *b1, const void *b2, int32_t *sel,
-               float *sel_score, void *ws, hipStream_t s) {
+int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *av, const void *b1, const void *b2,
+               int32_t *sel, float *sel_score, void *ws, hipStream_t s) {
   SelArgs a;
   a.a = av; a.b1 = b1; a.b2 = b2; a.sel = sel; a.sel_score = sel_score;
   a.an1 = a.an2 = a.bn1 = a.bn2 = nullptr;
   a.part = nullptr;
+  a.row0 = row0;
+  a.row1 = row1;
   sel_chunking(d->B, d->H, d->nblk, (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &a.ct, &a.nch);
   a.B = d->B; a.H = d->H; a.nblk = d->nblk; a.D = d->D; a.topk = d->topk; a.kk = d->kk;
   a.conv = d->convention; a.causal = d->causal; a.sink = d->sink; a.score = d->score;

@@ -63,10 +63,14 @@ SIGNATURES = {
     "fbsa_last_error": (ctypes.c_char_p, []),
     "fbsa_version": (ctypes.c_int, []),
     "fbsa_fwd": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fbsa_fwd_rows": (ctypes.c_int, [ctypes.POINTER(AttnDesc), ctypes.c_int64, ctypes.c_int64]
+                      + [_vp] * 9),
     "fbsa_pool": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _vp, _vp, _vp, _vp]),
     "fbsa_select_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SelectDesc)]),
     "fbsa_select": (ctypes.c_int, [ctypes.POINTER(SelectDesc), _vp, _vp, _vp, _vp, _vp, _vp,
                                    ctypes.c_size_t, _vp]),
+    "fbsa_select_rows": (ctypes.c_int, [ctypes.POINTER(SelectDesc), ctypes.c_int64, ctypes.c_int64,
+                                        _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "fbsa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnDesc)]),
     "fbsa_bwd_prep": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 6 + [ctypes.c_size_t, _vp]),
     "fbsa_transpose_index": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, ctypes.c_size_t, _vp]),

@@ -96,15 +96,10 @@ def _check_common(q, k, v, sel, gate):
         raise ValueError(f"fbsa: gate shape {tuple(gate.shape)} != sel shape {tuple(sel.shape)}")
 
 
-def attention_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None,
-                      out_gate=None, need_lse=False):
-    """Fused block-sparse attention forward.
-
-    q (B,Hq,L,D); k, v (B,Hkv,L,D); sel (B,Hsel,nblk,kk) integer block ids with
-    Hsel in {1, Hkv}; gate (B,Hsel,nblk,kk) additive bias (cast to fp32);
-    out_gate (B,Hq,L,D) (any strides): o <- o * sigmoid(out_gate).
-    Returns o (and the fp32 natural-log LSE (B,Hq,L) when need_lse).
-    """
+def prepare_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None, out_gate=None, need_lse=False):
+    """Checks and kernel-ready views for the forward, and its outputs (allocated,
+    not yet written). sel must already be the int32 tensor the kernel will read
+    (an int32 contiguous sel is used in place, so it may be filled later)."""
     _check_common(q, k, v, sel, gate)
     B, Hq, L, D = q.shape
     scale = D ** -0.5 if scale is None else scale
@@ -125,12 +120,40 @@ def attention_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None
     if sel32.shape[2] == 0 or L % sel32.shape[2]:
         raise ValueError(f"fbsa: L={L} is not a multiple of nblk={sel32.shape[2]}")
     d = make_desc(qk[0], qk[1], qk[2], o, sel32, mask=mask, scale=scale, l_valid=l_valid, out_gate=og)
+    return {"d": d, "qkv": qk, "sel": sel32, "gate": gate32, "og": og, "o": o, "lse": lse, "D": D, "Dp": Dp,
+            "nblk": sel32.shape[2]}
+
+
+def launch_forward(prep, blocks=None):
+    """Runs the forward of query blocks [i0, i1) (all when None) on the current stream."""
+    i0, i1 = (0, prep["nblk"]) if blocks is None else blocks
+    qk = prep["qkv"]
     lib = _lib.load()
-    _lib.check(lib.fbsa_fwd(d, _ptr(qk[0]), _ptr(qk[1]), _ptr(qk[2]), _ptr(sel32), _ptr(gate32),
-                            _ptr(og), _ptr(o), _ptr(lse), _stream()), "fbsa_fwd")
-    if Dp != D:
-        o = o[..., :D]
-    return (o, lse) if need_lse else o
+    _lib.check(lib.fbsa_fwd_rows(prep["d"], i0, i1, _ptr(qk[0]), _ptr(qk[1]), _ptr(qk[2]), _ptr(prep["sel"]),
+                                 _ptr(prep["gate"]), _ptr(prep["og"]), _ptr(prep["o"]), _ptr(prep["lse"]),
+                                 _stream()), "fbsa_fwd")
+
+
+def finish_forward(prep, need_lse):
+    o = prep["o"]
+    if prep["Dp"] != prep["D"]:
+        o = o[..., :prep["D"]]
+    return (o, prep["lse"]) if need_lse else o
+
+
+def attention_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None,
+                      out_gate=None, need_lse=False):
+    """Fused block-sparse attention forward.
+
+    q (B,Hq,L,D); k, v (B,Hkv,L,D); sel (B,Hsel,nblk,kk) integer block ids with
+    Hsel in {1, Hkv}; gate (B,Hsel,nblk,kk) additive bias (cast to fp32);
+    out_gate (B,Hq,L,D) (any strides): o <- o * sigmoid(out_gate).
+    Returns o (and the fp32 natural-log LSE (B,Hq,L) when need_lse).
+    """
+    prep = prepare_forward(q, k, v, sel, mask=mask, scale=scale, gate=gate, l_valid=l_valid, out_gate=out_gate,
+                           need_lse=need_lse)
+    launch_forward(prep)
+    return finish_forward(prep, need_lse)
 
 
 def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=None, l_valid=None,

@@ -54,7 +54,7 @@ def budget(convention, topk, nblk, sink=False):
 
 
 def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=True, sink=False,
-           need_scores=False, engine="auto", chunk_tiles=0):
+           need_scores=False, engine="auto", chunk_tiles=0, rows=None, out=None, workspace=None):
     """Top-k key blocks per query block from pooled operands (B,H,nblk,D).
 
     convention 'own_first' (A, src/ssa_model.py:151-165): [i, top-k content
@@ -65,6 +65,9 @@ def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=
     only where an MFMA bracket is ambiguous); "fp64" scores everything in fp64.
     Both return identical blocks. chunk_tiles (tuning/tests): candidate tiles
     of 64 blocks per workgroup on the MFMA path, 0 = chosen from the sizes.
+    rows=(r0, r1) selects query blocks [r0, r1) only, writing those rows of
+    `out` (an int32 (B,H,nblk,kk) tensor); `workspace` may pass a uint8
+    tensor of at least select_workspace_bytes() bytes to reuse.
     """
     _require_cuda(a, b1, b2)
     if a.dim() != 4 or a.shape != b1.shape or (b2 is not None and b2.shape != a.shape):
@@ -86,14 +89,35 @@ def select(a, b1, b2=None, *, score="dot", convention="own_first", topk, causal=
         raise ValueError("fbsa.select: chunk_tiles must be in [0, 65536)")
     d.flags = chunk_tiles << _lib.SEL_CHUNK_SHIFT
     d.B, d.H, d.nblk, d.D, d.topk, d.kk = B, H, nblk, D, topk, kk
-    sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
+    if out is not None:
+        if out.shape != (B, H, nblk, kk) or out.dtype != torch.int32 or not out.is_contiguous():
+            raise ValueError(f"fbsa.select: out must be contiguous int32 {(B, H, nblk, kk)}")
+        sel = out
+    else:
+        sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
     sc = torch.empty(B, H, nblk, kk, dtype=torch.float32, device=a.device) if need_scores else None
     lib = _lib.load()
     nbytes = lib.fbsa_select_workspace_bytes(d) if engine == "auto" else 0
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
-    _lib.check(lib.fbsa_select(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(sel), _ptr(sc), _ptr(ws), nbytes, _stream()),
-               "fbsa_select")
+    if workspace is not None and nbytes and workspace.numel() >= nbytes:
+        ws = workspace
+    else:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    r0, r1 = (0, nblk) if rows is None else rows
+    _lib.check(lib.fbsa_select_rows(d, r0, r1, _ptr(a), _ptr(b1), _ptr(b2), _ptr(sel), _ptr(sc), _ptr(ws), nbytes,
+                                    _stream()), "fbsa_select")
     return (sel, sc) if need_scores else sel
+
+
+def select_workspace_bytes(a, *, score="dot", convention="own_first", topk, sink=False, chunk_tiles=0):
+    """Workspace bytes the MFMA engine needs for pooled operands shaped like `a`."""
+    B, H, nblk, D = a.shape
+    d = _lib.SelectDesc()
+    d.dtype = _dtype_code(a)
+    d.score = SCORES[score]
+    d.convention = {"own_first": _lib.SEL_OWN_FIRST, "sorted_sink": _lib.SEL_SORTED_SINK}[convention]
+    d.causal, d.sink, d.flags = 1, 1 if sink else 0, chunk_tiles << _lib.SEL_CHUNK_SHIFT
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = B, H, nblk, D, topk, budget(convention, topk, nblk, sink)
+    return _lib.load().fbsa_select_workspace_bytes(d)
 
 
 def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False, engine="auto"):

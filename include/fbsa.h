@@ -77,6 +77,15 @@ int fbsa_fwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
              const int32_t *sel, const float *gate, const void *out_gate,
              void *o, float *lse, void *stream);
 
+/* The forward for query blocks [i_begin, i_end) only (O and LSE rows of those
+ * blocks are written; sel rows outside the range are not read). Lets a caller
+ * overlap the selection of later query blocks with the forward of earlier
+ * ones on two streams. fbsa_fwd is the range [0, nblk). No counterpart in
+ * the reference (its forward is one call over all blocks). */
+int fbsa_fwd_rows(const fbsa_attn_desc *d, int64_t i_begin, int64_t i_end, const void *q, const void *k,
+                  const void *v, const int32_t *sel, const float *gate, const void *out_gate, void *o,
+                  float *lse, void *stream);
+
 /* ---- selection ------------------------------------------------------- */
 
 /* Pooling ops over each block of bs tokens (tokens >= l_valid read as 0).
@@ -137,6 +146,14 @@ size_t fbsa_select_workspace_bytes(const fbsa_select_desc *d);
 int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2,
                 int32_t *sel, float *sel_score, void *workspace, size_t workspace_bytes,
                 void *stream);
+
+/* Selection for query blocks [row_begin, row_end) only (those rows of sel and
+ * sel_score are written). Causal selections of a prefix of rows read only
+ * that prefix of the operands. fbsa_select is the range [0, nblk). No
+ * counterpart in the reference (it selects all rows at once). */
+int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a,
+                     const void *b1, const void *b2, int32_t *sel, float *sel_score, void *workspace,
+                     size_t workspace_bytes, void *stream);
 
 /* ---- backward -------------------------------------------------------- */
 

@@ -107,6 +107,30 @@ def test_select_flags_and_workspace_size():
     assert lib.fbsa_select_workspace_bytes(d) == 0
 
 
+def test_row_range_entry_points_validate_ranges():
+    lib = _lib.load()
+    d = _lib.SelectDesc()
+    d.dtype, d.score, d.convention, d.causal = _lib.BF16, _lib.SCORE_DOT, _lib.SEL_OWN_FIRST, 1
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = 1, 1, 64, 64, 8, 9
+    for r0, r1 in ((-1, 10), (10, 5), (0, 65)):
+        assert lib.fbsa_select_rows(d, r0, r1, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EINVAL
+        assert "range" in lib.fbsa_last_error().decode()
+    a = _desc()
+    for r0, r1 in ((-1, 1), (3, 2), (0, a.nblk + 1)):
+        assert lib.fbsa_fwd_rows(a, r0, r1, DUMMY, DUMMY, DUMMY, DUMMY, None, None, DUMMY, None, None) == _lib.EINVAL
+        assert "range" in lib.fbsa_last_error().decode()
+
+
+def test_pipeline_row_splits_cover_rows():
+    from fbsa_amd.pipeline import _row_splits
+    for nblk in (1, 63, 64, 65, 700, 4096, 65536):
+        for splits in (1, 2, 4, 7):
+            r = _row_splits(nblk, splits)
+            assert r[0][0] == 0 and r[-1][1] == nblk
+            assert all(a < b for a, b in r) and all(r[x][1] == r[x + 1][0] for x in range(len(r) - 1))
+            assert all(a % 64 == 0 for a, _ in r)
+
+
 def test_python_ops_require_gpu_tensors():
     import torch
     from fbsa_amd import ops
