@@ -1307,9 +1307,72 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
 
+  // Pending entries -> exact keys, in place, for all 16 rows of the wave at
+  // once: lane p holds entries p, p + 16, p + 32, p + 48 of rows 16w + 4qb + g.
+  // The candidate norms of every pending entry are fetched together (one
+  // memory round trip instead of one per entry), the rounded bracket settles
+  // almost all of them, and the rest take the fp64 dot product.
+  {
+    uint32_t amb = 0;  // bit 4qb + e: entry left for the fp64 path
+    if constexpr (MODE != FBSA_SCORE_QUEST) {
+      uint64_t ke[4][4];
+      float bj[4][4];
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        const int q = 16 * w + 4 * qb + g, n = cnt[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ke[qb][e] = p + 16 * e < n ? buf[q][p + 16 * e] : 0;
+          bj[qb][e] = 0.f;
+          if (ke[qb][e] != 0 && !((uint32_t)ke[qb][e] & 0x80000000u)) {
+            const int64_t j = (int64_t)(uint32_t)ke[qb][e] - 1;
+            bj[qb][e] = a.bn1[bh * nbp + j];
+            if constexpr (MODE == FBSA_SCORE_MAX2) bj[qb][e] = fmaxf(bj[qb][e], a.bn2[bh * nbp + j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint64_t en = ke[qb][e];
+          if (en == 0 || ((uint32_t)en & 0x80000000u)) continue;
+          const int q = 16 * w + 4 * qb + g;
+          const float hi = __uint_as_float((uint32_t)(en >> 32));
+          const float beta = rown[0][q] * bj[qb][e];
+          const float rl = round_dt_f<T>(hi - 2.02f * beta), rh = round_dt_f<T>(hi);
+          if (rl == rh && isfinite(rh)) buf[q][p + 16 * e] = make_key(rh, (int)(uint32_t)en - 1);
+          else amb |= 1u << (4 * qb + e);
+        }
+    } else {
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) {
+        const int q = 16 * w + 4 * qb + g, n = cnt[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint64_t en = p + 16 * e < n ? buf[q][p + 16 * e] : 0;
+          if (en != 0 && !((uint32_t)en & 0x80000000u)) amb |= 1u << (4 * qb + e);
+        }
+      }
+    }
+    // one exact_score_global() instance: the loop stays rolled
+#pragma unroll 1
+    while (amb) {
+      const int b = __builtin_ctz(amb);
+      amb &= amb - 1;
+      const int q = 16 * w + 4 * (b >> 2) + g, slot = p + 16 * (b & 3);
+      const int j = (int)(uint32_t)buf[q][slot] - 1;
+      buf[q][slot] = make_key(exact_score_global<T, D, MODE>(a, bh, r0 + q, j), j);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+  }
+
   // this chunk's top K of each row, 4 rows at a time (one per lane group):
   // lane p ranks keys p, p + 16, p + 32, p + 48 of its row against the row's
-  // buffer and stores the top K in descending order
+  // buffer. A single chunk stores them in descending order for emit_row();
+  // otherwise they go straight to the row's partial list (zeros past the
+  // row's entries), which the merge kernel combines.
+  const bool single = nchunks == 1;
 #pragma unroll 1
   for (int qb = 0; qb < 4; ++qb) {
     const int q = 16 * w + 4 * qb + g;
@@ -1317,10 +1380,6 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     const int nmax = __builtin_amdgcn_readfirstlane(
         max(max(__builtin_amdgcn_readlane(n, 0), __builtin_amdgcn_readlane(n, 16)),
             max(__builtin_amdgcn_readlane(n, 32), __builtin_amdgcn_readlane(n, 48))));
-    // pending entries -> exact keys, in place (one resolve() instance: the loop stays rolled)
-#pragma unroll 1
-    for (int e = p; e < n; e += 16) buf[q][e] = resolve(buf[q][e], q);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
     uint64_t k[4];
     int rk[4];
 #pragma unroll
@@ -1337,13 +1396,26 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) rk[e] += km[u] > k[e] ? 1 : 0;
     }
+    if (single) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (k[e] != 0 && rk[e] < K) buf[q][rk[e]] = k[e];
-    if (p == 0) cnt[q] = n < K ? n : K;
-    __builtin_amdgcn_s_waitcnt(0xC07F);
+      for (int e = 0; e < 4; ++e)
+        if (k[e] != 0 && rk[e] < K) buf[q][rk[e]] = k[e];
+      if (p == 0) cnt[q] = n < K ? n : K;
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+    } else {
+      const int64_t i = r0 + q;
+      if (i >= a.row0 && i < a.row1) {
+        uint64_t *dst = a.part + ((bh * a.nblk + i) * a.nch + ch) * K;
+        const int nk = n < K ? n : K;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (k[e] != 0 && rk[e] < K) dst[rk[e]] = k[e];
+          if (p + 16 * e >= nk && p + 16 * e < K) dst[p + 16 * e] = 0;
+        }
+      }
+    }
   }
-  const bool single = nchunks == 1;
+  if (!single) return;
   for (int qq = 0; qq < 16; ++qq) {
     const int q = 16 * w + qq;
     const int64_t i = r0 + q;
@@ -1351,8 +1423,7 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     if (i < a.row0) continue;
     const int n = __builtin_amdgcn_readfirstlane(cnt[q]);
     const uint64_t v = lane < n ? buf[q][lane] : 0;
-    if (single) emit_row<T, D, MODE>(a, bh, i, v, lane, K);
-    else if (lane < K) a.part[((bh * a.nblk + i) * a.nch + ch) * K + lane] = v;
+    emit_row<T, D, MODE>(a, bh, i, v, lane, K);
   }
 }
 
@@ -1384,17 +1455,30 @@ __global__ __launch_bounds__(256) void select_merge_kernel(SelArgs a) {
   emit_row<T, D, MODE>(a, bh, i, v, lane, K);
 }
 
-// Candidate tiles per workgroup: about 2048 workgroups over the row blocks,
-// chunks of at least 32 tiles (each chunk pays a fixed cost for its bound and
-// its final cut); a nonzero override (descriptor flags) wins.
-static void sel_chunking(int64_t B, int64_t H, int64_t nblk, int64_t override_ct, int64_t *ct, int64_t *nch) {
+// Candidate tiles per workgroup (chunk). Every chunk pays a fixed cost (its
+// pass-1 bound, the cut of its buffers, its partial list, a merge), and a short
+// chunk keeps more candidates (its bound comes from fewer tiles), so rows are
+// cut into chunks only when the row blocks alone would leave the GPU idle:
+// about two workgroups per CU (512 on MI355X's 256 CUs) at one workgroup of 64
+// rows per resident slot, chunks of at least 8 tiles, and no chunk longer than
+// half an even share of all tiles over those slots (the longest chunk sets the
+// kernel's tail). `tri`: row block r has r + 1 candidate tiles (causal or
+// convention B), else every row block has all of them. A nonzero override
+// (descriptor flags) wins.
+static void sel_chunking(int64_t B, int64_t H, int64_t nblk, bool tri, int64_t override_ct, int64_t *ct,
+                         int64_t *nch) {
   const int64_t ntiles = (nblk + 63) / 64;
   const int64_t rbs = B * H * ntiles;
   int64_t c = override_ct;
   if (c <= 0) {
-    const int64_t want = (2048 + rbs - 1) / rbs;
+    const int64_t slots = 512;
+    const int64_t want = (slots + rbs - 1) / rbs;  // chunks per row block
     c = (ntiles + want - 1) / want;
-    if (c < 32) c = 32;
+    const int64_t total = tri ? B * H * (ntiles * (ntiles + 1) / 2) : rbs * ntiles;
+    int64_t cap = (total + 2 * slots - 1) / (2 * slots);
+    if (cap < 64) cap = 64;  // rows of up to 64 tiles stay whole when the row blocks fill the GPU
+    if (c > cap) c = cap;
+    if (c < 8) c = 8;
   }
   *ct = c;
   *nch = (ntiles + c - 1) / c;
@@ -1466,7 +1550,8 @@ size_t select_workspace_bytes(const fbsa_select_desc *d) {
   if (d->dtype == FBSA_F32 || (d->D != 32 && d->D != 64)) return 0;
   const int64_t n = d->B * d->H * d->nblk;
   int64_t ct, nch;
-  sel_chunking(d->B, d->H, d->nblk, (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &ct, &nch);
+  sel_chunking(d->B, d->H, d->nblk, d->causal || d->convention != FBSA_SEL_OWN_FIRST,
+               (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &ct, &nch);
   const int64_t K = d->topk < d->nblk ? d->topk : d->nblk;
   return (size_t)(4 * d->B * d->H * sel_norm_pitch(d->nblk)) * sizeof(float) + 256 +
          (size_t)(n * nch * (K > 0 ? K : 1)) * sizeof(uint64_t);
@@ -1480,7 +1565,8 @@ int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void
   a.part = nullptr;
   a.row0 = row0;
   a.row1 = row1;
-  sel_chunking(d->B, d->H, d->nblk, (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &a.ct, &a.nch);
+  sel_chunking(d->B, d->H, d->nblk, d->causal || d->convention != FBSA_SEL_OWN_FIRST,
+               (d->flags >> FBSA_SEL_CHUNK_SHIFT) & 0xFFFF, &a.ct, &a.nch);
   a.B = d->B; a.H = d->H; a.nblk = d->nblk; a.D = d->D; a.topk = d->topk; a.kk = d->kk;
   a.conv = d->convention; a.causal = d->causal; a.sink = d->sink; a.score = d->score;
   switch (d->dtype) {

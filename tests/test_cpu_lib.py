@@ -103,6 +103,13 @@ def test_select_flags_and_workspace_size():
     assert auto >= 4 * npad * 4
     d.flags = 4 << _lib.SEL_CHUNK_SHIFT   # 16 chunks of 4 tiles: larger partial-list area
     assert lib.fbsa_select_workspace_bytes(d) == 4 * npad * 4 + 256 + 8 * 4096 * 16 * 16 * 8
+    # automatic chunking: rows are cut into chunks (of at least 8 tiles) only
+    # when the row blocks alone leave the GPU idle
+    d.flags = 0
+    assert auto == 4 * npad * 4 + 256 + 8 * 4096 * 1 * 16 * 8      # 512 row blocks: whole rows
+    d.H = 1
+    assert lib.fbsa_select_workspace_bytes(d) == 4 * 4096 * 4 + 256 + 4096 * 8 * 16 * 8  # 64 row blocks: 8 chunks
+    d.H = 8
     d.dtype = _lib.F32   # fp32 operands take the fp64 engine: no workspace
     assert lib.fbsa_select_workspace_bytes(d) == 0
 
