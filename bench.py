@@ -38,7 +38,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--N", type=int, default=262144)
     p.add_argument("--H", type=int, default=8)
     p.add_argument("--D", type=int, default=64)

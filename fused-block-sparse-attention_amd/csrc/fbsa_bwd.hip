@@ -541,15 +541,24 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
       }
       tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
       float pp[C::KC / 16][4], ds[C::KC / 16][4];
+      float2 ms[C::KC / 16][4];
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ms[m][r] = Ms[16 * m + 4 * g + r];
+      // every exponential is computed and masked by a select: a conditional
+      // exponential becomes a branch per element, each waiting for its own
+      // row-statistics read
 #pragma unroll
       for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float2 ms = Ms[16 * m + 4 * g + r];
           const bool ok = kok && (16 * m + r >= tmin);
-          const float pv = ok ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x)) : 0.f;
+          float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms[m][r].x));
+          asm volatile("" : "+v"(ev));
+          const float pv = ok ? ev : 0.f;
           pp[m][r] = pv;
-          ds[m][r] = pv * (dpacc[m][r] - ms.y);
+          ds[m][r] = pv * (dpacc[m][r] - ms[m][r].y);
         }
       mm_tr_acc<T, D, C::KC>(Ds, pp, dvacc, g, p);  // dV^T += dO^T P
       mm_tr_acc<T, D, C::KC>(Qs, ds, dkacc, g, p);  // dK^T += Q^T dS
