@@ -271,7 +271,7 @@ template <typename T, int BS, int D, int BUDGET, int META> struct BwdCfg {
   static constexpr int NCH = BS / KC;
   static constexpr int CPR = D * ES / 16;
   static constexpr int TILE_BYTES = KC * D * ES;
-  static constexpr int META_BYTES = META ? NW * KC * 8 : 0;  // per-wave copies of (lse2, delta) rows
+  static constexpr int META_BYTES = META ? KC * 8 : 0;  // the chunk's (lse2, delta) rows, a quarter per wave
   static constexpr int STAGE_BYTES = 2 * TILE_BYTES + META_BYTES;
   static constexpr int LPT = 2 * TILE_BYTES / (NT * 16);
   static constexpr int NS0 = BUDGET / STAGE_BYTES;
@@ -443,9 +443,10 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 }
 
 template <typename T, int BS, int D>
-__global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 3 : 1) void dkdv_kernel(BwdArgs a) {
   using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
   constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
+  constexpr int HR = C::KC >= 64 ? 32 : C::KC;  // query rows per part of a chunk
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
   int *s_i = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
@@ -501,8 +502,10 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
       issue_tile_pair<T, C::KC, D, C::NW, C::LPT>(st, (const T *)a.q + b * a.sq[0] + hq * a.sq[1], a.sq[2],
                                                   (const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1], a.sdo[2], row0,
                                                   w, lane);
-      if (lane < C::KC / 2)
-        g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + 2 * lane, st + 2 * C::TILE_BYTES + w * (C::KC * 8));
+      // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
+      if (lane < C::KC / (2 * C::NW))
+        g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + w * (C::KC / C::NW) + 2 * lane,
+                st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
     };
 #pragma unroll
     for (int c = 0; c < C::NSTAGE - 1; ++c)
@@ -519,15 +522,11 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
 
       const char *Qs = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
       const char *Ds = Qs + C::TILE_BYTES;
-      const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES + w * (C::KC * 8));
+      const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
       const int x = (c / C::NCH) / a.grp, ch = c % C::NCH;
       const int kind = s_kind[x];
       const float gt = s_gate[x];
       const int64_t i = s_i[x];
-
-      f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
-      mm_rows_frag<T, D, C::KC / 16>(Qs, kf, sacc, g, p);   // S: query 16m+4g+r, key u
-      mm_rows_frag<T, D, C::KC / 16>(Ds, vf, dpacc, g, p);  // dP
 
       // valid iff query row (within block i) >= tmin, and the key is in range
       int tmin = -(1 << 30);
@@ -540,28 +539,36 @@ __global__ __launch_bounds__(BS * 4) void dkdv_kernel(BwdArgs a) {
         kok = keyok;
       }
       tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
-      float pp[C::KC / 16][4], ds[C::KC / 16][4];
-      float2 ms[C::KC / 16][4];
+
+      // the chunk's query rows in parts of HR (32) rows, one after the other:
+      // the per-part S, dP, P, dS and row statistics stay in few registers
+#pragma unroll 1
+      for (int h = 0; h < C::KC / HR; ++h) {
+        const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
+        const float2 *Mh = Ms + h * HR;
+        const int th = tmin - h * HR;
+        f32x4 sacc[HR / 16], dpacc[HR / 16];
+        mm_rows_frag<T, D, HR / 16>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
+        mm_rows_frag<T, D, HR / 16>(Dh, vf, dpacc, g, p);  // dP
+        float pp[HR / 16][4], ds[HR / 16][4];
+        // every exponential is computed and masked by a select: a conditional
+        // exponential becomes a branch per element, each waiting for its own
+        // row-statistics read
 #pragma unroll
-      for (int m = 0; m < C::KC / 16; ++m)
+        for (int m = 0; m < HR / 16; ++m)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ms[m][r] = Ms[16 * m + 4 * g + r];
-      // every exponential is computed and masked by a select: a conditional
-      // exponential becomes a branch per element, each waiting for its own
-      // row-statistics read
-#pragma unroll
-      for (int m = 0; m < C::KC / 16; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool ok = kok && (16 * m + r >= tmin);
-          float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms[m][r].x));
-          asm volatile("" : "+v"(ev));
-          const float pv = ok ? ev : 0.f;
-          pp[m][r] = pv;
-          ds[m][r] = pv * (dpacc[m][r] - ms[m][r].y);
-        }
-      mm_tr_acc<T, D, C::KC>(Ds, pp, dvacc, g, p);  // dV^T += dO^T P
-      mm_tr_acc<T, D, C::KC>(Qs, ds, dkacc, g, p);  // dK^T += Q^T dS
+          for (int r = 0; r < 4; ++r) {
+            const float2 ms = Mh[16 * m + 4 * g + r];
+            const bool ok = kok && (16 * m + r >= th);
+            float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x));
+            asm volatile("" : "+v"(ev));
+            const float pv = ok ? ev : 0.f;
+            pp[m][r] = pv;
+            ds[m][r] = pv * (dpacc[m][r] - ms.y);
+          }
+        mm_tr_acc<T, D, HR>(Dh, pp, dvacc, g, p);  // dV^T += dO^T P
+        mm_tr_acc<T, D, HR>(Qh, ds, dkacc, g, p);  // dK^T += Q^T dS
+      }
     }
   }
 
