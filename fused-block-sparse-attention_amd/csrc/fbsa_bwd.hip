@@ -41,7 +41,7 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #define FBSA_DQ_LDS_BUDGET 32768
 #endif
 #ifndef FBSA_DKDV_LDS_BUDGET
-#define FBSA_DKDV_LDS_BUDGET 61440
+#define FBSA_DKDV_LDS_BUDGET 40960
 #endif
 
 static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }
@@ -442,16 +442,18 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   }
 }
 
+// Latency bound (each chunk is a short chain of LDS reads, MFMAs and
+// exponentials), so occupancy decides: for bs 64 with 16-bit d <= 64 the
+// kernel is held to four waves per SIMD (at most 128 VGPRs) and its two-stage
+// ring (35 KB of LDS) fits four workgroups per CU.
 template <typename T, int BS, int D>
-__global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 3 : 1) void dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4 : 1) void dkdv_kernel(BwdArgs a) {
   using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
   constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
   constexpr int HR = C::KC >= 64 ? 32 : C::KC;  // query rows per part of a chunk
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
-  int *s_i = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
-  int *s_kind = s_i + MAXE;
-  float *s_gate = (float *)(s_kind + MAXE);
+  int4 *s_meta = (int4 *)(smem + C::NSTAGE * C::STAGE_BYTES);  // per entry: query block, mask kind, gate bits
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
   const int64_t total = a.B * a.Hkv * a.nblk;
@@ -477,6 +479,22 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 3
     dvacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Direct-to-LDS copy plan for a chunk's Q / dO tile pair: which tensor each
+  // of this thread's LPT loads reads is uniform across the wave (a tile is a
+  // whole number of 1 KiB wave-loads) and its byte offset from the chunk's
+  // first row is fixed, so an issue is a scalar base plus a precomputed offset.
+  int32_t toff[C::LPT];
+  bool tdo[C::LPT];
+#pragma unroll
+  for (int n = 0; n < C::LPT; ++n) {
+    const int u = (n * C::NW + w) * 64 + lane;
+    const int part = u / (C::KC * C::CPR);
+    const int rem = u - part * (C::KC * C::CPR);
+    const int row = rem / C::CPR, pos = rem % C::CPR;
+    toff[n] = (int32_t)(((int64_t)row * (part ? a.sdo[2] : a.sq[2]) + (pos ^ swz(row, C::CPR)) * (16 / C::ES)) * C::ES);
+    tdo[n] = part != 0;
+  }
+
   for (int eb = e0; eb < e1; eb += MAXE) {
     const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
     __syncthreads();  // the previous batch's entries are no longer read
@@ -488,29 +506,37 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 3
       else if (a.mask == FBSA_MASK_NONE) kind = (j + 1) * BS > a.l_valid ? KIND_PAD : KIND_FULL;
       else if (a.mask == FBSA_MASK_TOKEN_CAUSAL)
         kind = (j == i || (j + 1) * BS > a.l_valid) ? KIND_ABS : KIND_FULL;
-      s_i[x] = i;
-      s_kind[x] = kind;
-      s_gate[x] = a.gate ? a.gate[((b * a.hsel + hs) * a.nblk + i) * a.kk + s] * kLog2e : 0.f;
+      const float gt = a.gate ? a.gate[((b * a.hsel + hs) * a.nblk + i) * a.kk + s] * kLog2e : 0.f;
+      s_meta[x] = int4{i, kind, __float_as_int(gt), 0};
     }
     __syncthreads();
+    // chunk c = (entry, query head of the group, KC-row chunk), the chunk index fastest;
+    // the issue side and the compute side each step their own counters (no divisions)
     const int nchunks = ne * a.grp * C::NCH;
-    auto issue = [&](int c) {
-      const int task = c / C::NCH, ch = c % C::NCH;
-      const int x = task / a.grp, hq = hk * a.grp + task % a.grp;
-      const int64_t row0 = (int64_t)s_i[x] * BS + ch * C::KC;
-      char *st = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
-      issue_tile_pair<T, C::KC, D, C::NW, C::LPT>(st, (const T *)a.q + b * a.sq[0] + hq * a.sq[1], a.sq[2],
-                                                  (const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1], a.sdo[2], row0,
-                                                  w, lane);
+    int ix = 0, ig = 0, ic = 0, istg = 0;  // next chunk to issue and its stage
+    auto issue = [&]() {
+      const int hq = hk * a.grp + ig;
+      const int64_t row0 = (int64_t)s_meta[ix].x * BS + ic * C::KC;
+      const char *qb = (const char *)a.q + (b * a.sq[0] + hq * a.sq[1] + row0 * a.sq[2]) * C::ES;
+      const char *db = (const char *)a.dout + (b * a.sdo[0] + hq * a.sdo[1] + row0 * a.sdo[2]) * C::ES;
+      char *st = stages + istg * C::STAGE_BYTES;
+#pragma unroll
+      for (int n = 0; n < C::LPT; ++n) g2lds16((tdo[n] ? db : qb) + toff[n], st + (n * C::NW + w) * 1024);
       // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
       if (lane < C::KC / (2 * C::NW))
         g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + w * (C::KC / C::NW) + 2 * lane,
                 st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
+      if (++ic == C::NCH) {
+        ic = 0;
+        if (++ig == a.grp) { ig = 0; ++ix; }
+      }
+      if (++istg == C::NSTAGE) istg = 0;
     };
 #pragma unroll
     for (int c = 0; c < C::NSTAGE - 1; ++c)
-      if (c < nchunks) issue(c);
+      if (c < nchunks) issue();
 
+    int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
     for (int c = 0; c < nchunks; ++c) {
       // stage c has landed for this wave (LPT + 1 loads per stage; up to NSTAGE - 2 later
       // stages may still be in flight); after the barrier every wave's part has landed and
@@ -518,15 +544,21 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 3
       const int ahead = nchunks - 1 - c;
       wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
       lds_barrier();
-      if (c + C::NSTAGE - 1 < nchunks) issue(c + C::NSTAGE - 1);
+      if (c + C::NSTAGE - 1 < nchunks) issue();
 
-      const char *Qs = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
+      const char *Qs = stages + cstg * C::STAGE_BYTES;
       const char *Ds = Qs + C::TILE_BYTES;
       const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
-      const int x = (c / C::NCH) / a.grp, ch = c % C::NCH;
-      const int kind = s_kind[x];
-      const float gt = s_gate[x];
-      const int64_t i = s_i[x];
+      const int4 meta = s_meta[cx];
+      const int ch = cch;
+      const int kind = meta.y;
+      const float gt = __int_as_float(meta.z);
+      const int64_t i = meta.x;
+      if (++cch == C::NCH) {
+        cch = 0;
+        if (++cg == a.grp) { cg = 0; ++cx; }
+      }
+      if (++cstg == C::NSTAGE) cstg = 0;
 
       // valid iff query row (within block i) >= tmin, and the key is in range
       int tmin = -(1 << 30);
@@ -648,7 +680,7 @@ template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipS
 
 template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
   using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 12;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16;
   static size_t granted = 0;
   int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
   if (e) return e;

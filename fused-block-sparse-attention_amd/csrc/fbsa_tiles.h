@@ -81,28 +81,35 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
       for (int r = 0; r < 4; ++r) { y[r] = x[2 * k2][r]; y[4 + r] = x[2 * k2 + 1][r]; }
       pk[k2] = pack8<T>(y);
     }
-    s16x4 lo[D / 16][KC / 32], hi[D / 16][KC / 32];
+    // the transposed reads go out in batches of up to 8 output tiles (all of
+    // them for d <= 128), each batch waited for once, so d = 256 does not hold
+    // every tile's operands in registers at the same time
+    constexpr int TB = D / 16 < 8 ? D / 16 : 8;
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-      const int cb = 2 * t + ((p & 3) >> 1);
+    for (int t0 = 0; t0 < D / 16; t0 += TB) {
+      s16x4 lo[TB][KC / 32], hi[TB][KC / 32];
 #pragma unroll
-      for (int k2 = 0; k2 < KC / 32; ++k2) {
-        const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
-        lo[t][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
-        hi[t][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
+      for (int tt = 0; tt < TB; ++tt) {
+        const int cb = 2 * (t0 + tt) + ((p & 3) >> 1);
+#pragma unroll
+        for (int k2 = 0; k2 < KC / 32; ++k2) {
+          const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
+          lo[tt][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
+          hi[tt][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
+        }
       }
+      lds_wait_all();
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+        for (int k2 = 0; k2 < KC / 32; ++k2) {
+          lds_ready(lo[tt][k2]);
+          lds_ready(hi[tt][k2]);
+          const s16x4 a = lo[tt][k2], b = hi[tt][k2];
+          const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+          acc[t0 + tt] = Mfma16<T>::run(av, pk[k2], acc[t0 + tt]);
+        }
     }
-    lds_wait_all();
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int k2 = 0; k2 < KC / 32; ++k2) {
-        lds_ready(lo[t][k2]);
-        lds_ready(hi[t][k2]);
-        const s16x4 a = lo[t][k2], b = hi[t][k2];
-        const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        acc[t] = Mfma16<T>::run(av, pk[k2], acc[t]);
-      }
   } else {
     s16x4 pk;
 #pragma unroll
