@@ -145,4 +145,24 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
   return (bid % 8) * per + bid / 8;
 }
 
+// Launch order of query-major kernels with grouped query heads: work unit u
+// (b, KV head, query block) goes to XCD u % 8 (round-robin, like plain launch
+// order) and its grp query-head workgroups run back to back on that XCD, so the
+// K/V tiles they share are fetched into one L2 once instead of into grp of
+// them. Returns the unit of launch order bid and sets the head within the
+// group; with grp == 1 it is the identity. Units past the last full round of 8
+// map in launch order.
+__device__ __forceinline__ int64_t gqa_unit(int64_t bid, int64_t nunits, int grp, int *hin) {
+  const int64_t full = nunits / 8 * 8;
+  const int64_t base = full * grp;
+  if (bid >= base) {
+    const int64_t r = bid - base;
+    *hin = (int)(r % grp);
+    return full + r / grp;
+  }
+  const int64_t s = bid / 8;
+  *hin = (int)(s % grp);
+  return (s / grp) * 8 + bid % 8;
+}
+
 }  // namespace fbsa

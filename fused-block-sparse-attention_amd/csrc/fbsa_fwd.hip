@@ -74,11 +74,12 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   __shared__ int s_nvalid;
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, p = lane & 15;
-  // launch order: consecutive workgroups are the query heads of one KV group,
-  // then consecutive query blocks (round-robin over the XCDs measured faster
-  // for the gathered K/V than XCD-contiguous ranges)
-  int64_t t = blockIdx.x;
-  const int hin = (int)(t % a.grp); t /= a.grp;
+  // launch order: consecutive query blocks round-robin over the XCDs
+  // (measured faster for the gathered K/V than XCD-contiguous ranges), the
+  // query heads of one KV group back to back on one XCD (they share the K/V
+  // tiles)
+  int hin;
+  int64_t t = gqa_unit(blockIdx.x, (int64_t)gridDim.x / a.grp, a.grp, &hin);
   const int64_t i = a.i0 + t % a.ni; t /= a.ni;
   const int hk = (int)(t % a.Hkv);
   const int64_t b = t / a.Hkv;
