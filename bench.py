@@ -14,8 +14,8 @@ Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step;
 ``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
 FLOP per launch, the reference's own formula, src/bench_crossover.py:105)
 timed with HIP events on the launch stream in separate, unoverlapped
-launches; ``cpu_baseline`` times the CPU oracle (numpy restatement of the
-reference gather path) on a bounded sample of query blocks and scales it to
+launches; ``cpu_baseline`` times the reference's PyTorch gather path on the
+host cores (same dtype) on a bounded sample of query blocks and scales it to
 the whole workload.
 """
 import argparse
@@ -49,7 +49,7 @@ def parse():
                    help="time the two-stream step (selection overlapped with the forward)")
     p.add_argument("--splits", type=int, default=4, help="row ranges of the overlapped step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    p.add_argument("--cpu-rows", type=int, default=128, help="query blocks in the CPU sample")
+    p.add_argument("--cpu-rows", type=int, default=4096, help="query blocks in the CPU sample (4096 = all at config 3)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     return p.parse_args()
@@ -79,38 +79,66 @@ def traffic_from_profiles(kernel, workload):
 
 
 def cpu_baseline(q, k, v, bs, topk, rows_wanted):
-    """Time the CPU oracle on a bounded sample: full pooling, then scores +
-    convention-A selection + gather attention for `rows_wanted` query blocks
-    spread over the sequence; scale to the whole workload."""
-    import numpy as np
-    from oracle import attn as oattn, select as osel
+    """The reference's PyTorch path on the host cores, in the same dtype: block
+    pooling (mean over tokens, then heads, src/ssa_model.py:287-288), scores
+    qpool kpool^T and convention A (own block + top-k strictly past blocks,
+    src/ssa_model.py:151-165), then the gather path: selected K/V blocks
+    gathered per query block, additive mask (slot 0 causal triu, slots > 0
+    valid iff block < i) and SDPA (src/ssa_model.py:57-90, 167-183). Pooling
+    runs over the whole sequence; scores, top-k and attention over a bounded
+    sample of `rows_wanted` query blocks spread over the sequence (chunks of 64),
+    scaled to all blocks. Threads: torch's intra-op pool (the box sets
+    OMP_NUM_THREADS to its CPU share)."""
+    import torch
+    import torch.nn.functional as F
 
-    f64 = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
-    qh, kh, vh = f64(q), f64(k), f64(v)
-    B, H, N, D = qh.shape
+    nthreads = torch.get_num_threads()
+    qc, kc, vc = (t.detach().cpu() for t in (q, k, v))
+    B, H, N, D = qc.shape
     nblk = N // bs
-    rows = np.unique(np.linspace(0, nblk - 1, rows_wanted).astype(np.int64))
+    rows = torch.linspace(0, nblk - 1, rows_wanted).round().long().unique()
+    NEG = torch.finfo(torch.float32).min
     t0 = time.perf_counter()
-    qp = osel.pool_mean_tok_then_heads(qh, bs, "bf16")
-    kp = osel.pool_mean_tok_then_heads(kh, bs, "bf16")
+    qpool = qc.view(B, H, nblk, bs, D).mean(3).mean(1)  # (B, nblk, D)
+    kpool = kc.view(B, H, nblk, bs, D).mean(3).mean(1)
     t_pool = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    raw = osel.scores(qp, kp, "bf16", "dot", rows=rows)
-    sel = osel.select_conv_a(raw, topk, True, rows=rows)
-    t_sel = time.perf_counter() - t0
-    full_sel = np.zeros((B, nblk, sel.shape[-1]), dtype=np.int64)
-    full_sel[:, rows] = sel
-    t0 = time.perf_counter()
-    oattn.fwd(qh, kh, vh, full_sel[:, None], "slot_causal", rows=rows)
-    t_fwd = time.perf_counter() - t0
+
+    t_sel = t_fwd = 0.0
+    kb = kc.view(B, H, nblk, bs, D)
+    vb = vc.view(B, H, nblk, bs, D)
+    qb = qc.view(B, H, nblk, bs, D)
+    kk_c = min(topk, nblk - 1)
+    ar = torch.arange(nblk)
+    tri = torch.zeros(bs, (kk_c + 1) * bs)
+    tri[:, :bs] = torch.triu(torch.full((bs, bs), NEG), 1)
+    for c0 in range(0, len(rows), 64):
+        r = rows[c0:c0 + 64]
+        t0 = time.perf_counter()
+        raw = torch.matmul(qpool[:, r], kpool.transpose(1, 2))  # (B, R, nblk)
+        content = raw.masked_fill(ar.view(1, 1, nblk) >= r.view(1, -1, 1), float("-inf"))
+        sel = torch.cat([r.view(1, -1, 1).expand(B, -1, 1), content.topk(kk_c, dim=-1).indices], dim=-1)
+        t_sel += time.perf_counter() - t0
+        t0 = time.perf_counter()
+        R, kk = sel.shape[1], sel.shape[2]
+        bi = torch.arange(B).view(B, 1, 1, 1)
+        hi = torch.arange(H).view(1, H, 1, 1)
+        si = sel.view(B, 1, R, kk)
+        ks = kb[bi, hi, si].reshape(B, H, R, kk * bs, D)
+        vs = vb[bi, hi, si].reshape(B, H, R, kk * bs, D)
+        valid = torch.ones(B, R, kk, dtype=torch.bool)
+        valid[..., 1:] = sel[..., 1:] < r.view(1, -1, 1)
+        blk = torch.zeros(B, R, kk).masked_fill_(~valid, NEG).repeat_interleave(bs, dim=-1).unsqueeze(2)
+        mask = (blk + tri).unsqueeze(1).to(qc.dtype)  # (B, 1, R, bs, kk*bs)
+        F.scaled_dot_product_attention(qb[:, :, r], ks, vs, attn_mask=mask)
+        t_fwd += time.perf_counter() - t0
     scale = nblk / len(rows)
     total = t_pool + (t_sel + t_fwd) * scale
     return {
-        "value": B * N / total, "unit": "tokens/s", "cores": 1, "kind": "port",
-        "sample": (f"numpy float64 oracle: full q/k pooling ({t_pool:.2f} s) + scores, top-k and "
-                   f"gather attention for {len(rows)} of {nblk} query blocks x {H} heads "
-                   f"({t_sel + t_fwd:.2f} s), scaled x{scale:.1f} to all blocks; "
-                   f"est. {total:.1f} s per step"),
+        "value": B * N / total, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+        "sample": (f"torch {str(qc.dtype).replace('torch.', '')} on {nthreads} host threads, the reference's "
+                   f"gather path: full q/k pooling ({t_pool:.2f} s) + scores, top-k and gather attention for "
+                   f"{len(rows)} of {nblk} query blocks x {H} heads ({t_sel + t_fwd:.2f} s), scaled "
+                   f"x{scale:.1f} to all blocks; est. {total:.1f} s per step"),
     }
 
 
