@@ -207,15 +207,19 @@ def main():
     achieved = flops / (t_fwd * 1e-3) / 1e12
     wl = f"cfg3_N{N}_H{H}_D{D}_bs{bs}_top{topk}"
     gathered = B * H * nblk * kk * 2 * bs * D * 2
+    shape = (H, D, bs, topk)
+    cfg_name = ("BASELINE configs[2]" if (N, shape) == (262144, (8, 64, 64, 16))
+                else "BASELINE configs[4] (selection-scaling stress)" if (N, shape) == (4194304, (8, 64, 64, 16))
+                else "custom shape")
     out = {
-        "metric": "select+fwd tokens/s at 262k tokens, 1 GPU (bf16, H8 D64 bs64 top-16, causal)",
+        "metric": (f"select+fwd tokens/s at {N // 1000}k tokens, 1 GPU (bf16, H{H} D{D} bs{bs} top-{topk}, causal)"),
         "value": B * N / (ms_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": ms_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (q,k,v ~ N(0,1)/sqrt(D), seed 0, device generator)",
-        "config": {"workload": "BASELINE configs[2]: block-pair selection (mean-pooled q.k, top-16, "
+        "config": {"workload": f"{cfg_name}: block-pair selection (mean-pooled q.k, top-{topk}, "
                                "own-first) + fused block-sparse forward, causal",
                    "B": B, "H": H, "N": N, "D": D, "block": bs, "nblk": nblk, "topk": topk, "kk": kk,
                    "step": (f"selection overlapped with the forward ({a.splits} row ranges, 2 streams)" if a.overlap
