@@ -148,6 +148,7 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
   if (d->convention != FBSA_SEL_OWN_FIRST && d->convention != FBSA_SEL_SORTED_SINK)
     return fail(FBSA_EINVAL, "fbsa_select: bad convention %d", d->convention);
   if (d->B < 1 || d->H < 1 || d->nblk < 1 || d->topk < 0) return fail(FBSA_EINVAL, "fbsa_select: bad sizes");
+  if (d->nblk > 0x7fffffffLL - 64) return fail(FBSA_EUNSUPPORTED, "fbsa_select: nblk %lld exceeds 32-bit block indices", (long long)d->nblk);
   if (d->flags & ~(0xFFFF << FBSA_SEL_CHUNK_SHIFT)) return fail(FBSA_EINVAL, "fbsa_select: unknown flags 0x%x", d->flags);
   int64_t K, kk;
   if (d->convention == FBSA_SEL_OWN_FIRST) { K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1; kk = 1 + K; }

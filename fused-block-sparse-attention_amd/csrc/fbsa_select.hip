@@ -955,15 +955,17 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   // consecutive work items (same head) on one XCD, so its L2 holds that head's candidates
   int64_t x = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t ch = x % a.nch; x /= a.nch;
-  const int64_t rb = rb1 - 1 - x % nrr;  // heavy (late) row blocks first
+  // tile and block indices fit 32 bits (the host rejects nblk >= 2^31 - 64)
+  const int rb = (int)(rb1 - 1 - x % nrr);  // heavy (late) row blocks first
   const int64_t bh = x / nrr;
-  const int64_t r0 = rb * 64;
+  const int r0 = rb * 64;
   const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
-  const int64_t last_row = r0 + 63 < a.nblk - 1 ? r0 + 63 : a.nblk - 1;
-  const int64_t jmax = (a.causal || !convA) ? last_row : a.nblk - 1;
-  const int64_t ntiles = jmax / 64 + 1;
-  const int64_t nchunks = (ntiles + a.ct - 1) / a.ct;
-  const int64_t t0 = ch * a.ct, t1 = t0 + a.ct < ntiles ? t0 + a.ct : ntiles;
+  const int nb = (int)a.nblk, ct = (int)a.ct;
+  const int last_row = r0 + 63 < nb - 1 ? r0 + 63 : nb - 1;
+  const int jmax = (a.causal || !convA) ? last_row : nb - 1;
+  const int ntiles = jmax / 64 + 1;
+  const int nchunks = (ntiles + ct - 1) / ct;
+  const int t0 = (int)ch * ct, t1 = t0 + ct < ntiles ? t0 + ct : ntiles;
   if (t0 >= t1) return;  // uniform: this chunk is past the row block's candidates
   const int nt = (int)(t1 - t0);
   const int K = (int)(convA ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1) : (a.topk < a.nblk ? a.topk : a.nblk));
@@ -1026,10 +1028,10 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     drow[n] = row;
     doff[n] = (uint32_t)((row * D + (pos ^ swz(row, C::CPR)) * 8) * 2);
   }
-  auto issue = [&](int64_t tile, int stg) {
+  auto issue = [&](int tile, int stg) {
     char *st = ring + stg * C::STB;
-    const int64_t j0 = tile * 64;
-    const int lim = (int)(a.nblk - 1 - j0 < 63 ? a.nblk - 1 - j0 : 63);  // last real candidate row
+    const int j0 = tile * 64;
+    const int lim = nb - 1 - j0 < 63 ? nb - 1 - j0 : 63;  // last real candidate row
 #pragma unroll
     for (int n = 0; n < C::LPT; ++n) {
       const int op = (n * 4 + w) / C::CPR;
@@ -1098,13 +1100,13 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   };
 
   // validity of (row 4g + r, candidate 16t + p) on a diagonal or ragged tile: bit 4t + r
-  const int ilim = (int)(a.nblk - r0 < 64 ? a.nblk - r0 : 64);
+  const int ilim = nb - r0 < 64 ? nb - r0 : 64;
   uint32_t rowmask = 0;  // rows of this lane that exist (the last row block may be ragged)
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     if (16 * w + 4 * g + r < ilim) rowmask |= 0x1111u << r;
-  auto valid_mask = [&](int64_t tl) {
-    const int jlim = (int)(a.nblk - tl * 64 < 64 ? a.nblk - tl * 64 : 64);
+  auto valid_mask = [&](int tl) {
+    const int jlim = nb - tl * 64 < 64 ? nb - tl * 64 : 64;
     const bool diag = tl == rb;
     const int dm = !diag ? 0 : convA ? (a.causal ? 1 : 2) : 3;  // none, j < i, j != i, j <= i
     uint32_t vm = 0;
@@ -1129,17 +1131,17 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
 
   // Tile order within each pass: the full off-diagonal tiles first, then the
   // (at most two) diagonal / ragged tiles, so those get loop bodies of their own.
-  const int64_t big = INT64_MAX / 4;
-  int64_t m1 = rb >= t0 && rb < t1 ? rb : big;                               // diagonal
-  int64_t m2 = (a.nblk & 63) && t1 == (a.nblk + 63) / 64 ? t1 - 1 : big;  // ragged last tile
+  const int big = INT32_MAX / 4;
+  int m1 = rb >= t0 && rb < t1 ? rb : big;                          // diagonal
+  int m2 = (nb & 63) && t1 == (nb + 63) / 64 ? t1 - 1 : big;  // ragged last tile
   if (m2 == m1) m2 = big;
-  if (m2 < m1) { const int64_t tmp = m1; m1 = m2; m2 = tmp; }
+  if (m2 < m1) { const int tmp = m1; m1 = m2; m2 = tmp; }
   const int nm = (m1 != big) + (m2 != big);
   const int nu = nt - nm;
-  auto tile_of = [&](int k) -> int64_t {  // stage k: tile of pass k / nt
+  auto tile_of = [&](int k) -> int {  // stage k: tile of pass k / nt
     const int kk = k < nt ? k : k - nt;
     if (kk >= nu) return kk == nu ? m1 : m2;
-    int64_t u = t0 + kk;
+    int u = t0 + kk;
     if (u >= m1) ++u;
     if (u >= m2) ++u;
     return u;
@@ -1153,7 +1155,7 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
   auto step = [&](int it, auto masked_c, auto collect_c) {
     constexpr bool MASKED = decltype(masked_c)::value, COLLECT = decltype(collect_c)::value;
     const int stg = it % NST;
-    const int64_t tl = tile_of(it);
+    const int tl = tile_of(it);
     // this wave's loads of stage it have landed (LPT + 1 per stage; later stages may be in flight)
     const int ahead = 2 * nt - 1 - it < NST - 2 ? 2 * nt - 1 - it : NST - 2;
     wait_ring<C::LPT + 1>(ahead);
@@ -1161,7 +1163,7 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
     if (it + NST - 1 < 2 * nt) issue(tile_of(it + NST - 1), (it + NST - 1) % NST);
     const char *st = ring + stg * C::STB;
     const float *nrm = (const float *)(st + C::NOP * C::OPB);
-    const int64_t j0 = tl * 64;
+    const int j0 = tl * 64;
 
     s16x8 bfr[C::NOP][4][C::KS];
     s16x8 bp[C::NOP][4];
