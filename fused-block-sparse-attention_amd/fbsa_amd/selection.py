@@ -146,3 +146,56 @@ def select_quest(q, k, bs, topk, sink=True, l_valid=None, engine="auto"):
     qpool = pool(q, bs, "mean_grp_then_tok", grp=grp, l_valid=l_valid)
     kmin, kmax = pool(k, bs, "minmax", l_valid=l_valid)
     return select(qpool, kmax, kmin, score="quest", convention="sorted_sink", topk=topk, sink=sink, engine=engine)
+
+
+def _pool_last_token(q, bs, grp):
+    """Last token of every query block, averaged over the GQA group:
+    ``q.view(B,Hkv,grp,nblk,bs,d).mean(2)[:, :, :, -1, :]``
+    (src/qwen_blocksparse.py:268). A ragged last block's last token is the zero
+    padding. Pools the strided view of those tokens with bs = 1."""
+    B, Hq, L, D = q.shape
+    nblk = (L + bs - 1) // bs
+    full = L // bs
+    out = torch.zeros(B, Hq // grp, nblk, D, dtype=q.dtype, device=q.device)
+    if full:
+        out[:, :, :full] = pool(q[:, :, bs - 1:full * bs:bs], 1, "mean_grp_then_tok", grp=grp)
+    return out
+
+
+def select_quest_lasttok(q, k, bs, topk, sink=True, engine="auto"):
+    """SelectLastTok (src/qwen_blocksparse.py:256-275): the Quest score of each
+    query block's last token (mean over its GQA group) against the per-block
+    key min/max, then ``_finish``. Returns idx (B, Hkv, nblk, kk) int32."""
+    Hkv = k.shape[1]
+    grp = q.shape[1] // Hkv
+    qlast = _pool_last_token(q, bs, grp)
+    kmin, kmax = pool(k, bs, "minmax")
+    return select(qlast, kmax, kmin, score="quest", convention="sorted_sink", topk=topk, sink=sink, engine=engine)
+
+
+def select_learned(q, k, Wq, Wk, bs, topk, sink=True, scale=None, minmax=False, engine="auto"):
+    """SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:171-212):
+    block-pooled q (group mean, then token mean) and k (token mean, or the
+    per-block [kmin, kmax]) projected through Wq / Wk (torch matmuls, as the
+    reference), then the top-k of scale * sq.sk^T with ``_finish``. A positive
+    scale does not change the order; the selection streams rnd(sq.sk) (exact,
+    rounded to the operand dtype) and never forms the nblk x nblk matrix.
+    Returns idx (B, Hkv, nblk, kk) int32."""
+    Hkv = k.shape[1]
+    grp = q.shape[1] // Hkv
+    scale = float(Wq.shape[1] ** -0.5) if scale is None else float(scale)
+    qpool = pool(q, bs, "mean_grp_then_tok", grp=grp)
+    if minmax:
+        kmin, kmax = pool(k, bs, "minmax")
+        kfeat = torch.cat([kmin, kmax], dim=-1)
+    else:
+        kfeat = pool(k, bs, "mean_tok_then_grp", grp=1)
+    sq = qpool.to(Wq.dtype) @ Wq
+    sk = kfeat.to(Wk.dtype) @ Wk
+    if scale < 0:
+        sk = -sk  # rnd(-x) = -rnd(x): the order of scale * s is the order of -s
+    elif scale == 0:
+        sq = torch.zeros_like(sq)  # every score is 0
+    return select(sq.contiguous(), sk.contiguous(), score="dot", convention="sorted_sink", topk=topk, sink=sink,
+                  engine=engine)
+

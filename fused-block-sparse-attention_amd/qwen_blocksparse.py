@@ -15,7 +15,10 @@ Same surface as ``src/qwen_blocksparse.py``:
   ``out_gate`` (B, Hq, L, d) applies ``o * sigmoid(out_gate)`` in the
   kernel's epilogue (the Qwen output gate, ``src/patch_qwen.py:55``).
 * ``SelectMax`` (``:102-121``): Quest min/max upper-bound selector on the
-  pooling and streaming top-k kernels; ``SelectAll`` (``:155-165``).
+  pooling and streaming top-k kernels; ``SelectLastTok`` (``:256-275``, the
+  same score from each block's last token); ``SelectLearned`` /
+  ``SelectLearnedMinMax`` (``:171-212``, pooled features through Wq / Wk, the
+  projections in torch as in the reference); ``SelectAll`` (``:155-165``).
 * ``_pad_blocks`` and ``_finish`` (``:20-26``, ``:87-99``) and the
   dense-score selectors ``SelectOracle`` / ``SelectRandom`` (``:124-152``),
   kept for callers that build their own score matrix.
@@ -91,6 +94,44 @@ class SelectMax:
     @torch.no_grad()
     def select(self, q, k):
         return selection.select_quest(q, k, self.bs, self.topk, sink=self.sink).long()
+
+
+class SelectLastTok:
+    """SelectMax scored by each query block's last token (its GQA-group mean)
+    instead of the block mean (``src/qwen_blocksparse.py:256-275``); pooling and
+    the streaming top-k run on the GPU kernels."""
+
+    def __init__(self, topk, bs, sink=True):
+        self.topk, self.bs, self.sink = topk, bs, sink
+
+    @torch.no_grad()
+    def select(self, q, k):
+        return selection.select_quest_lasttok(q, k, self.bs, self.topk, sink=self.sink).long()
+
+
+class SelectLearned:
+    """Learned selector: block-pooled q / k projected through Wq / Wk (d, sel_dim),
+    top-k of scale * sq.sk^T (``src/qwen_blocksparse.py:171-189``)."""
+
+    def __init__(self, Wq, Wk, topk, bs, sink=True, scale=None):
+        self.Wq, self.Wk = Wq, Wk
+        self.topk, self.bs, self.sink = topk, bs, sink
+        self.scale = float(Wq.shape[1] ** -0.5) if scale is None else float(scale)
+
+    @torch.no_grad()
+    def select(self, q, k):
+        return selection.select_learned(q, k, self.Wq, self.Wk, self.bs, self.topk, sink=self.sink,
+                                        scale=self.scale).long()
+
+
+class SelectLearnedMinMax(SelectLearned):
+    """SelectLearned with the per-block key [kmin, kmax] (2d features) through Wk
+    (2d, sel_dim) instead of the key mean (``src/qwen_blocksparse.py:192-212``)."""
+
+    @torch.no_grad()
+    def select(self, q, k):
+        return selection.select_learned(q, k, self.Wq, self.Wk, self.bs, self.topk, sink=self.sink,
+                                        scale=self.scale, minmax=True).long()
 
 
 class SelectAll:

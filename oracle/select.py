@@ -8,6 +8,8 @@ Restates, in numpy, the reference's block-pair selection:
 * ``pool_mean_grp_then_tok`` / ``pool_minmax`` -- ``SelectMax.select``
   (``src/qwen_blocksparse.py:111-116``).
 * ``pool_tok`` -- ``BlockSparseSSA._scores`` pooling (``src/ssa_model.py:114-117``).
+* ``pool_last_token_grp`` / ``pool_mean_tok`` -- the ``SelectLastTok`` and
+  ``SelectLearned`` poolings (``src/qwen_blocksparse.py:268``, ``:181-182``).
 * ``scores`` -- the nblk x nblk contraction: plain dot (``src/scale_sel.py:33``),
   max of two dots (``src/ssa_model.py:118-119``), Quest q+/q- split
   (``src/qwen_blocksparse.py:117-120``), each rounded where torch rounds.
@@ -68,6 +70,28 @@ def pool_minmax(k, bs):
     k, nblk = _pad_tokens(k, bs, 2)
     kb = k.reshape(B, H, nblk, bs, D)
     return kb.min(axis=3), kb.max(axis=3)
+
+
+def pool_last_token_grp(q, hkv, bs, dtype):
+    """(B,Hq,N,D) -> (B,Hkv,nblk,D): the GQA-group mean (rounded) of each
+    block's last token; a ragged last block's last token is the zero padding.
+    ``q.view(B,Hkv,grp,nblk,bs,d).mean(2)[:, :, :, -1, :]``
+    (``src/qwen_blocksparse.py:268``)."""
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, N, D = q.shape
+    grp = Hq // hkv
+    q, nblk = _pad_tokens(q, bs, 2)
+    last = q.reshape(B, Hq, nblk, bs, D)[:, :, :, -1, :]
+    return round_to(last.reshape(B, hkv, grp, nblk, D).sum(axis=2) / grp, dtype)
+
+
+def pool_mean_tok(x, bs, dtype):
+    """(B,H,N,D) -> (B,H,nblk,D): per-head token mean (rounded), zero padding
+    counted: ``kp.view(B,Hkv,nblk,bs,d).mean(3)`` (``src/qwen_blocksparse.py:182``)."""
+    x = np.asarray(x, dtype=np.float64)
+    B, H, N, D = x.shape
+    x, nblk = _pad_tokens(x, bs, 2)
+    return round_to(x.reshape(B, H, nblk, bs, D).sum(axis=3) / bs, dtype)
 
 
 def pool_tok(x, bs, dtype, op):
@@ -211,6 +235,26 @@ def select_quest(q, k, bs, topk, sink, dtype):
     kmin, kmax = pool_minmax(k, bs)
     sc = scores(qpool, kmax, dtype, "quest", b2=kmin)
     return select_conv_b(sc, topk, sink), sc
+
+
+def select_quest_lasttok(q, k, bs, topk, sink, dtype):
+    """``SelectLastTok.select`` (``src/qwen_blocksparse.py:262-275``): Quest
+    scores of each block's last-token group mean, then ``_finish``."""
+    hkv = k.shape[1]
+    qlast = pool_last_token_grp(q, hkv, bs, dtype)
+    kmin, kmax = pool_minmax(k, bs)
+    sc = scores(qlast, kmax, dtype, "quest", b2=kmin)
+    return select_conv_b(sc, topk, sink), sc
+
+
+def select_learned_features(sq, sk, topk, sink, dtype, scale):
+    """``SelectLearned`` / ``SelectLearnedMinMax`` from their projected features
+    (``src/qwen_blocksparse.py:185-189``, ``:208-212``): score =
+    rnd(scale * rnd(sq . sk)) in the feature dtype, then ``_finish``. Returns
+    (idx, score, unscaled rnd(sq . sk))."""
+    raw = scores(sq, sk, dtype, "dot")
+    sc = round_to(scale * raw, dtype)
+    return select_conv_b(sc, topk, sink), sc, raw
 
 
 def near_tie_rows(score, sel_valid_sets, k_eff, valid_mask, rel=1e-6):

@@ -251,3 +251,57 @@ def test_qwen_selectmax_forward_matches_oracle_with_outgate(dtype):
                               out_gate=og.to(DEV))
     ro, _ = oattn.fwd(pad(q), pad(k), pad(v), ref_idx, "token_causal", scale=0.1, L_valid=L, out_gate=pad(og))
     assert_close(np64(out), ro[:, :, :L], dtype, "out")
+
+
+@pytest.mark.parametrize("L,d,dtype", [(2048, 64, "bf16"), (2000, 128, "bf16"), (1024, 64, "f32")])
+def test_qwen_select_lasttok_matches_oracle(L, d, dtype):
+    # SelectLastTok (src/qwen_blocksparse.py:256-275): Quest score of each block's
+    # last-token group mean; the ragged block's last token is zero padding
+    from qwen_blocksparse import SelectLastTok
+    g = torch.Generator().manual_seed(21)
+    B, Hq, Hkv, bs, topk = 1, 8, 2, 64, 6
+    q, k = randn(g, (B, Hq, L, d), dtype), randn(g, (B, Hkv, L, d), dtype)
+    _say("lasttok", L, d, dtype)
+    idx = SelectLastTok(topk=topk, bs=bs, sink=True).select(q.to(DEV), k.to(DEV)).cpu().numpy()
+    ref, _ = osel.select_quest_lasttok(np64(q), np64(k), bs, topk, True, dtype)
+    assert idx.shape == ref.shape and np.array_equal(idx, ref)
+
+
+@pytest.mark.parametrize("minmax", [False, True])
+@pytest.mark.parametrize("sel_dim,dtype", [(64, "bf16"), (32, "bf16"), (64, "f32")])
+def test_qwen_select_learned_matches_oracle(minmax, sel_dim, dtype):
+    # SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:171-212): pooled
+    # features (checked against the oracle's pools) projected by torch as in the
+    # reference, then the streaming top-k of scale * sq.sk^T. With sel_dim 64 the
+    # default scale is 1/8 (exact); with 32 it rounds, and may merge neighbouring
+    # scores into exact ties, where the chosen score multiset must still agree.
+    from fbsa_amd import selection
+    from qwen_blocksparse import SelectLearned, SelectLearnedMinMax
+    g = torch.Generator().manual_seed(22)
+    B, Hq, Hkv, L, d, bs, topk = 1, 8, 2, 4096, 64, 64, 8
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    q, k = randn(g, (B, Hq, L, d), dtype).to(DEV), randn(g, (B, Hkv, L, d), dtype).to(DEV)
+    Wq = (torch.randn(d, sel_dim, generator=g) / 8).to(tdt).to(DEV)
+    Wk = (torch.randn(2 * d if minmax else d, sel_dim, generator=g) / 8).to(tdt).to(DEV)
+    S = (SelectLearnedMinMax if minmax else SelectLearned)(Wq, Wk, topk=topk, bs=bs, sink=True)
+    _say("learned", minmax, sel_dim, dtype)
+    idx = S.select(q, k).cpu().numpy()
+    qpool = selection.pool(q, bs, "mean_grp_then_tok", grp=Hq // Hkv)
+    np.testing.assert_array_equal(np64(qpool), osel.pool_mean_grp_then_tok(np64(q), Hkv, bs, dtype))
+    if minmax:
+        kmin, kmax = selection.pool(k, bs, "minmax")
+        kfeat = torch.cat([kmin, kmax], -1)
+        omin, omax = osel.pool_minmax(np64(k), bs)
+        np.testing.assert_array_equal(np64(kfeat), np.concatenate([omin, omax], -1))
+    else:
+        kfeat = selection.pool(k, bs, "mean_tok_then_grp", grp=1)
+        np.testing.assert_array_equal(np64(kfeat), osel.pool_mean_tok(np64(k), bs, dtype))
+    sq, sk = np64(qpool @ Wq), np64(kfeat @ Wk)
+    ref, sc, _ = osel.select_learned_features(sq, sk, topk, True, dtype, S.scale)
+    if sel_dim == 64:
+        assert np.array_equal(idx, ref)
+    else:
+        got_sc = np.sort(np.take_along_axis(sc, idx, -1), -1)
+        ref_sc = np.sort(np.take_along_axis(sc, ref, -1), -1)
+        assert np.array_equal(got_sc, ref_sc)
+        assert (idx == ref).all(-1).mean() > 0.9

@@ -66,6 +66,45 @@ def test_pool_mean_matches_torch_cpu(dtype):
             np.testing.assert_allclose(g_, r_, rtol=4e-7 * 64, atol=1e-8)
 
 
+@pytest.mark.parametrize("N", [512, 500])
+def test_pool_last_token_and_token_mean_match_torch_cpu(N):
+    # the reference's expressions (src/qwen_blocksparse.py:268, :182) on the same bf16 data
+    B, Hq, Hkv, D, bs = 2, 4, 2, 32, 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, Hq, N, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16)
+    nblk = (N + bs - 1) // bs
+    qp = torch.nn.functional.pad(q, (0, 0, 0, nblk * bs - N))
+    kp = torch.nn.functional.pad(k, (0, 0, 0, nblk * bs - N))
+    ref_last = qp.view(B, Hkv, Hq // Hkv, nblk, bs, D).mean(2)[:, :, :, -1, :].double().numpy()
+    ref_mean = kp.view(B, Hkv, nblk, bs, D).mean(3).double().numpy()
+    got_last = osel.pool_last_token_grp(q.double().numpy(), Hkv, bs, "bf16")
+    got_mean = osel.pool_mean_tok(k.double().numpy(), bs, "bf16")
+    # a 2-term group mean is exact in fp32 before the bf16 rounding: identical
+    np.testing.assert_array_equal(got_last, ref_last)
+    if N % bs:
+        assert np.all(got_last[:, :, -1] == 0)  # the ragged block's last token is padding
+    diff = got_mean != ref_mean  # a 64-term fp32 sum may round differently at a bf16 midpoint
+    assert diff.mean() < 2e-3
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(ref_mean[diff]))) - 7)
+    assert np.all(np.abs(got_mean[diff] - ref_mean[diff]) <= ulp)
+
+
+def test_learned_scale_rounding_and_order():
+    # a positive scale keeps the order of rnd(sq.sk); it can only merge neighbours
+    # into exact ties (then the lower index wins); scale = 1/8 changes nothing
+    rng = np.random.default_rng(3)
+    sq = on.round_bf16(rng.standard_normal((1, 1, 40, 32)))
+    sk = on.round_bf16(rng.standard_normal((1, 1, 40, 32)))
+    idx8, sc8, raw = osel.select_learned_features(sq, sk, 6, True, "bf16", 0.125)
+    np.testing.assert_array_equal(sc8, raw * 0.125)
+    np.testing.assert_array_equal(idx8, osel.select_conv_b(raw, 6, True))
+    idx3, sc3, _ = osel.select_learned_features(sq, sk, 6, True, "bf16", 3 ** -0.5)
+    assert np.all(np.diff(np.sort(sc3.ravel())) >= 0)
+    order_ok = (np.sign(np.subtract.outer(raw.ravel(), raw.ravel())) * np.sign(np.subtract.outer(sc3.ravel(), sc3.ravel()))) >= 0
+    assert order_ok.all()  # no inversions, only merges
+
+
 def test_pool_closed_forms():
     B, H, N, D, bs = 1, 2, 96, 8, 32
     c = RNG.standard_normal((B, H, N // bs, 1, D))
