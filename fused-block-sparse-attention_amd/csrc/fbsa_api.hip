@@ -108,6 +108,23 @@ int fbsa_fwd_rows(const fbsa_attn_desc *d, int64_t i_begin, int64_t i_end, const
   return run_fwd(d, a, (hipStream_t)stream);
 }
 
+size_t fbsa_block_mass_workspace_bytes(const fbsa_attn_desc *d) {
+  return d ? (size_t)(d->B * d->Hq * d->L) * sizeof(float) : 0;
+}
+
+int fbsa_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float *mass, void *ws, void *stream) {
+  int e = check_attn(d, "fbsa_block_mass");
+  if (e) return e;
+  if (d->dtype == FBSA_F32) return fail(FBSA_EUNSUPPORTED, "fbsa_block_mass: 16-bit operands only (bf16, f16)");
+  if ((d->bs != 64 && d->bs != 128) || d->D < 64)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_block_mass: needs bs in {64, 128} and D in {64, 128, 256}");
+  if (d->l_valid != d->L) return fail(FBSA_EINVAL, "fbsa_block_mass: L must be a whole number of blocks (l_valid = L)");
+  if (!q || !k || !mass || !ws) return fail(FBSA_EINVAL, "fbsa_block_mass: null pointer");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(mass, 4) || !aligned(ws, 16))
+    return fail(FBSA_EINVAL, "fbsa_block_mass: misaligned pointer");
+  return run_block_mass(d, q, k, mass, (float *)ws, (hipStream_t)stream);
+}
+
 int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, void *stream) {
   if (!d) return fail(FBSA_EINVAL, "fbsa_pool: null descriptor");
   if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_pool: bad dtype %d", d->dtype);

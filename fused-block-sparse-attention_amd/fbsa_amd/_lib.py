@@ -65,6 +65,8 @@ SIGNATURES = {
     "fbsa_fwd": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "fbsa_fwd_rows": (ctypes.c_int, [ctypes.POINTER(AttnDesc), ctypes.c_int64, ctypes.c_int64]
                       + [_vp] * 9),
+    "fbsa_block_mass_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnDesc)]),
+    "fbsa_block_mass": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _vp, _vp]),
     "fbsa_pool": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _vp, _vp, _vp, _vp]),
     "fbsa_select_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(SelectDesc)]),
     "fbsa_select": (ctypes.c_int, [ctypes.POINTER(SelectDesc), _vp, _vp, _vp, _vp, _vp, _vp,

@@ -214,3 +214,39 @@ def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=Non
         dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
         dog = dog[..., :D] if dog is not None else None
     return dq, dk, dv, dgate, dog
+
+
+def block_mass(q, k, bs, scale=None):
+    """Dense causal per-block attention mass (B, Hq, nblk, nblk) fp32 on the GPU
+    kernel: entry (i, j) is the mean over query block i's rows t of the softmax
+    probability summed over key block j's keys s <= t, zero above the diagonal
+    (``capture_mass``, src/eval_qwen_ppl.py:65-108, before its group mean).
+    Scores are rnd(rnd(q.k) * scale) in q's dtype, as torch's 16-bit matmul
+    rounds them; the softmax is fp32. q (B, Hq, L, D), k (B, Hkv, L, D) bf16 or
+    fp16, L a multiple of bs (64 or 128), D in {64, 128, 256}."""
+    _require_cuda(q, k)
+    if q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+        raise ValueError("fbsa.block_mass: q (B,Hq,L,D) and k (B,Hkv,L,D) expected")
+    if q.dtype != k.dtype or q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("fbsa.block_mass: q and k must both be bf16 or both fp16")
+    B, Hq, L, D = q.shape
+    if Hq % k.shape[1]:
+        raise ValueError(f"fbsa.block_mass: Hq={Hq} not a multiple of Hkv={k.shape[1]}")
+    if L % bs:
+        raise ValueError(f"fbsa.block_mass: L={L} is not a multiple of bs={bs}")
+    scale = D ** -0.5 if scale is None else scale
+    qk = [_kernel_ready(t) for t in (q, k)]
+    nblk = L // bs
+    d = _lib.AttnDesc()
+    d.dtype, d.mask = _dtype_code(q), _lib.MASK_TOKEN_CAUSAL
+    d.B, d.Hq, d.Hkv, d.L, d.D = B, Hq, k.shape[1], L, D
+    d.bs, d.nblk, d.kk, d.hsel, d.l_valid = bs, nblk, 1, 1, L
+    d.scale, d.flags = float(scale), 0
+    d.sq[:] = _strides3(qk[0])
+    d.sk[:] = _strides3(qk[1])
+    lib = _lib.load()
+    mass = torch.empty(B, Hq, nblk, nblk, dtype=torch.float32, device=q.device)
+    ws = torch.empty((lib.fbsa_block_mass_workspace_bytes(d) + 3) // 4, dtype=torch.float32, device=q.device)
+    _lib.check(lib.fbsa_block_mass(d, _ptr(qk[0]), _ptr(qk[1]), _ptr(mass), _ptr(ws), _stream()), "fbsa_block_mass")
+    return mass
+

@@ -19,6 +19,8 @@ Same surface as ``src/qwen_blocksparse.py``:
   same score from each block's last token); ``SelectLearned`` /
   ``SelectLearnedMinMax`` (``:171-212``, pooled features through Wq / Wk, the
   projections in torch as in the reference); ``SelectAll`` (``:155-165``).
+* ``block_mass`` -- the true block mass ``SelectOracle`` selects from (the
+  ``capture_mass`` loop of ``src/eval_qwen_ppl.py:84-95``) on a fused kernel.
 * ``_pad_blocks`` and ``_finish`` (``:20-26``, ``:87-99``) and the
   dense-score selectors ``SelectOracle`` / ``SelectRandom`` (``:124-152``),
   kept for callers that build their own score matrix.
@@ -64,6 +66,19 @@ def blocksparse_forward(q, k, v, *, selector, topk, bs, causal=True, scale=None,
     out = block_sparse_attention(qp, kp, vp, idx.to(torch.int32).contiguous(), mask=mask, scale=scale,
                                  out_gate=og, l_valid=L)
     return out[..., :L, :] if pad else out
+
+
+def block_mass(q, k, bs, scale=None):
+    """True block attention mass (B, Hkv, nblk, nblk) for ``SelectOracle``: the
+    dense causal softmax probability of each query block summed per key block,
+    averaged over the block's rows and over each KV head's query heads (the
+    ``capture_mass`` loop of src/eval_qwen_ppl.py:84-95, fused on the GPU: no
+    L x L matrix, no per-block Python loop). q (B, Hq, L, d) post-RoPE, k
+    (B, Hkv, L, d), L a multiple of bs; scale as passed to the attention."""
+    B, Hq, L, d = q.shape
+    Hkv = k.shape[1]
+    m = ops.block_mass(q, k, bs, scale)
+    return m.view(B, Hkv, Hq // Hkv, L // bs, L // bs).mean(2)
 
 
 def _finish(score, topk, sink, B, Hkv, nblk, dev):

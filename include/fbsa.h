@@ -86,6 +86,19 @@ int fbsa_fwd_rows(const fbsa_attn_desc *d, int64_t i_begin, int64_t i_end, const
                   const void *v, const int32_t *sel, const float *gate, const void *out_gate, void *o,
                   float *lse, void *stream);
 
+/* Dense causal per-block attention mass, the teacher SelectOracle selects from
+ * (capture_mass, src/eval_qwen_ppl.py:65-108): mass (B, Hq, nblk, nblk) fp32,
+ * entry (i, j) = the mean over block i's query rows t of the softmax
+ * probability summed over block j's keys s <= t; zero above the diagonal (the
+ * caller averages over each KV head's query heads, as the reference does).
+ * Scores are rounded like torch's 16-bit matmul and scale multiply,
+ * rnd(rnd(q.k) * scale); the softmax is fp32. Reads d->dtype (bf16 or f16),
+ * B, Hq, Hkv, L = nblk * bs, D (64, 128, 256), bs (64, 128), nblk, scale, sq,
+ * sk. ws: fbsa_block_mass_workspace_bytes(d) bytes, 16-byte aligned (the row
+ * log-sum-exp). Replaces the per-query-block loop of capture_mass. */
+size_t fbsa_block_mass_workspace_bytes(const fbsa_attn_desc *d);
+int fbsa_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float *mass, void *ws, void *stream);
+
 /* ---- selection ------------------------------------------------------- */
 
 /* Pooling ops over each block of bs tokens (tokens >= l_valid read as 0).

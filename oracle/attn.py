@@ -275,3 +275,36 @@ def dense(q, k, v, causal, scale=None, L_valid=None):
     m = lg.max(-1, keepdims=True)
     p = np.exp(lg - m)
     return np.einsum("bhtu,bhud->bhtd", p, vr) / p.sum(-1, keepdims=True)
+
+
+def block_mass(q, k, bs, scale, dtype):
+    """Dense causal per-block attention mass (``capture_mass``,
+    ``src/eval_qwen_ppl.py:65-108``): for each query block i and key block j,
+    the mean over block i's query rows t of the softmax probability summed over
+    block j's keys s <= t, averaged over each KV head's query-head group.
+    Scores are rounded as torch's 16-bit matmul and scale multiply round them
+    (rnd(rnd(q.k) * scale) in ``dtype``; exact products, float64 sums), the
+    softmax is float64. q (B,Hq,L,D), k (B,Hkv,L,D), L = nblk*bs.
+    Returns (B, Hkv, nblk, nblk) float64, zero above the diagonal."""
+    from .numerics import round_to
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    B, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    grp = Hq // Hkv
+    nblk = L // bs
+    out = np.zeros((B, Hq, nblk, nblk))
+    kpos = np.arange(L)
+    for h in range(Hq):
+        kh = k[:, h // grp]
+        for i in range(nblk):
+            qi = q[:, h, i * bs:(i + 1) * bs]                       # (B, bs, D)
+            s = round_to(round_to(np.einsum("btd,bsd->bts", qi, kh), dtype) * scale, dtype)
+            qpos = i * bs + np.arange(bs)
+            s = np.where(kpos[None, None, :] > qpos[None, :, None], -np.inf, s)
+            s = s - s.max(-1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(-1, keepdims=True)
+            out[:, h, i] = p.reshape(B, bs, nblk, bs).sum(-1).mean(1)
+    return out.reshape(B, Hkv, grp, nblk, nblk).mean(2)
+

@@ -305,3 +305,27 @@ def test_qwen_select_learned_matches_oracle(minmax, sel_dim, dtype):
         ref_sc = np.sort(np.take_along_axis(sc, ref, -1), -1)
         assert np.array_equal(got_sc, ref_sc)
         assert (idx == ref).all(-1).mean() > 0.9
+
+
+@pytest.mark.parametrize("dtype,L,d,bs", [("bf16", 512, 64, 64), ("bf16", 1024, 256, 128),
+                                          ("f16", 512, 128, 64), ("bf16", 768, 64, 128)])
+def test_qwen_block_mass_matches_oracle(dtype, L, d, bs):
+    # the true block mass of capture_mass (src/eval_qwen_ppl.py:84-95) on the fused kernel
+    from qwen_blocksparse import SelectOracle, block_mass
+    g = torch.Generator().manual_seed(23)
+    B, Hq, Hkv, scale = 1, 4, 2, 0.1
+    q, k = randn(g, (B, Hq, L, d), dtype), randn(g, (B, Hkv, L, d), dtype)
+    _say("block mass", dtype, L, d, bs)
+    got = block_mass(q.to(DEV), k.to(DEV), bs, scale)
+    ref = oattn.block_mass(np64(q), np64(k), bs, scale, dtype)
+    m = got.cpu().numpy().astype(np.float64)
+    assert m.shape == ref.shape
+    assert np.all(np.triu(m, 1) == 0)
+    np.testing.assert_allclose(m.sum(-1), 1.0, atol=1e-4)
+    np.testing.assert_allclose(m, ref, atol=5e-5)
+    assert np.abs(m - ref).mean() < 2e-6
+    # SelectOracle on it (src/qwen_blocksparse.py:124-138)
+    topk = 3
+    idx = SelectOracle(topk=topk, bs=bs, sink=True, mass=got).select(None, None).cpu().numpy()
+    ridx = osel.select_conv_b(ref, topk, True)
+    assert (idx == ridx).all(-1).mean() > 0.97  # rows apart only at near-equal masses

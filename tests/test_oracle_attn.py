@@ -154,3 +154,47 @@ def test_bwd_row_partition_sums_to_full():
     b = oattn.bwd(q, k, v, sel, do, "slot_causal", rows=[1, 3, 4])
     for x, y, z in zip(full[:4], a[:4], b[:4]):
         np.testing.assert_allclose(x, y + z, rtol=1e-12, atol=1e-12)
+
+
+def test_block_mass_closed_forms():
+    # q = 0: every score is 0, so row t attends uniformly to keys 0..t
+    B, Hq, Hkv, L, D, bs = 1, 2, 1, 128, 16, 32
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((B, Hkv, L, D))
+    m0 = oattn.block_mass(np.zeros((B, Hq, L, D)), k, bs, 0.25, "bf16")
+    nblk = L // bs
+    ref = np.zeros((nblk, nblk))
+    for i in range(nblk):
+        for t in range(bs):
+            T = i * bs + t
+            for j in range(i + 1):
+                ref[i, j] += min(bs, T + 1 - j * bs) / (T + 1) / bs
+    np.testing.assert_allclose(m0[0, 0], ref, rtol=0, atol=1e-15)
+    # any input: each row of blocks sums to 1, zero above the diagonal
+    q = rng.standard_normal((B, Hq, L, D))
+    m = oattn.block_mass(q, k, bs, 0.25, "bf16")
+    np.testing.assert_allclose(m.sum(-1), 1.0, atol=1e-12)
+    assert np.all(np.triu(m[0, 0], 1) == 0)
+
+
+def test_block_mass_matches_reference_loop_in_torch_cpu():
+    # the capture_mass loop (src/eval_qwen_ppl.py:84-95) run by torch on the same bf16 data
+    B, Hq, Hkv, L, D, bs, scaling = 1, 4, 2, 256, 32, 64, 0.2
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(B, Hq, L, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16)
+    grp, nblk = Hq // Hkv, L // bs
+    kr = k.repeat_interleave(grp, 1)
+    kpos = torch.arange(L)
+    ablk = torch.zeros(B, Hq, nblk, nblk)
+    for i in range(nblk):
+        qi = q[:, :, i * bs:(i + 1) * bs, :]
+        s = (qi @ kr.transpose(-1, -2)) * scaling
+        qpos = i * bs + torch.arange(bs)
+        s = s.float().masked_fill(kpos[None, None, None, :] > qpos[None, None, :, None], float("-inf"))
+        ablk[:, :, i, :] = s.softmax(-1).view(B, Hq, bs, nblk, bs).sum(-1).mean(2)
+    ref = ablk.view(B, Hkv, grp, nblk, nblk).mean(2).double().numpy()
+    got = oattn.block_mass(q.double().numpy(), k.double().numpy(), bs, scaling, "bf16")
+    # fp32 softmax and torch's fp32 accumulator vs exact products: a bf16 score may sit one ulp apart
+    np.testing.assert_allclose(got, ref, atol=2e-4)
+    assert np.abs(got - ref).mean() < 5e-6
