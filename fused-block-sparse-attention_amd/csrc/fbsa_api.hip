@@ -185,6 +185,35 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
   return run_select(d, row_begin, row_end, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
 }
 
+int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2, const int32_t *cand,
+                     int32_t *sel, void *stream) {
+  if (!d) return fail(FBSA_EINVAL, "fbsa_select_qmax: null descriptor");
+  if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_select_qmax: bad dtype %d", d->dtype);
+  if (d->convention != FBSA_SEL_SORTED_SINK && d->convention != FBSA_SEL_SORTED_TOPK)
+    return fail(FBSA_EINVAL, "fbsa_select_qmax: convention %d is not SORTED_SINK or SORTED_TOPK", d->convention);
+  if (d->flags & ~FBSA_QMAX_EXACT) return fail(FBSA_EINVAL, "fbsa_select_qmax: unknown flags 0x%x", d->flags);
+  if (d->B < 1 || d->H < 1 || d->nblk < 1 || d->tok < 1 || d->topk < 0)
+    return fail(FBSA_EINVAL, "fbsa_select_qmax: bad sizes");
+  if (d->la < (d->nblk - 1) * d->tok + 1 || d->la > d->nblk * d->tok)
+    return fail(FBSA_EINVAL, "fbsa_select_qmax: la=%lld must cover blocks 0..nblk-1 (((nblk-1)*tok, nblk*tok])",
+                (long long)d->la);
+  if (d->D != 32 && d->D != 64 && d->D != 128 && d->D != 256)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: operand dim %lld not in {32,64,128,256}", (long long)d->D);
+  if (d->nblk > 65536) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: nblk %lld > 65536", (long long)d->nblk);
+  if (cand && d->ncand < 1) return fail(FBSA_EINVAL, "fbsa_select_qmax: ncand must be >= 1 with a candidate list");
+  const int64_t ncol = cand ? d->ncand : d->nblk;
+  if (ncol > 4096) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: %lld columns per row > 4096", (long long)ncol);
+  const int64_t K = d->topk < d->nblk ? d->topk : d->nblk;
+  const int64_t kk = d->convention == FBSA_SEL_SORTED_SINK ? K + 1 + (d->sink ? 1 : 0) : K;
+  if (kk < 1) return fail(FBSA_EINVAL, "fbsa_select_qmax: SORTED_TOPK needs topk >= 1");
+  if (d->kk != kk) return fail(FBSA_EINVAL, "fbsa_select_qmax: kk=%lld but the convention gives %lld", (long long)d->kk, (long long)kk);
+  if (!a || !b1 || !b2 || !sel) return fail(FBSA_EINVAL, "fbsa_select_qmax: null pointer");
+  if (!aligned(a, 16) || !aligned(b1, 16) || !aligned(b2, 16) || !aligned(sel, 4) || (cand && !aligned(cand, 4)))
+    return fail(FBSA_EINVAL, "fbsa_select_qmax: misaligned pointer (a, b1, b2 need 16 bytes)");
+  if (d->B * d->H * d->nblk > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: grid too large");
+  return run_select_qmax(d, a, b1, b2, cand, sel, (hipStream_t)stream);
+}
+
 }  // extern "C"
 
 // ---- backward ----

@@ -20,33 +20,9 @@
 
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
+#include "fbsa_round.h"
 
 namespace fbsa {
-
-// ---------------------------------------------------------------- rounding
-// torch rounds a bf16/fp16 reduction twice: the exact value to the fp32
-// accumulator, then fp32 -> dtype (both RNE). The fp32 step is kept opaque so
-// the compiler cannot fold the pair into one double -> 16-bit rounding, which
-// differs when the fp32 value lands exactly on a 16-bit midpoint.
-__device__ __forceinline__ float rne_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return __uint_as_float(0x7FC00000u);  // NaN
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return __uint_as_float(u & 0xFFFF0000u);
-}
-template <typename T> __device__ __forceinline__ float round_dt_f(float f) {
-  if constexpr (sizeof(T) == 4) return f;
-  else if constexpr (__is_same(T, bf16)) return rne_bf16(f);
-  else {
-    asm volatile("" : "+v"(f));
-    return (float)(T)f;
-  }
-}
-template <typename T> __device__ __forceinline__ float round_dt(double x) {
-  float f = (float)x;  // RNE to fp32
-  asm volatile("" : "+v"(f));
-  return round_dt_f<T>(f);
-}
 
 // ---------------------------------------------------------------- pooling
 struct PoolArgs {
@@ -56,36 +32,6 @@ struct PoolArgs {
   int64_t sx[3];
   int op;
 };
-
-// 16-bit pattern -> fp32 (exact)
-template <typename T> __device__ __forceinline__ float half_bits_to_f32(uint32_t h);
-template <> __device__ __forceinline__ float half_bits_to_f32<bf16>(uint32_t h) { return __uint_as_float(h << 16); }
-template <> __device__ __forceinline__ float half_bits_to_f32<f16>(uint32_t h) {
-  const unsigned short hs = (unsigned short)h;
-  _Float16 x;
-  __builtin_memcpy(&x, &hs, 2);
-  return (float)x;
-}
-
-// 8 consecutive elements (16 bytes) -> fp64
-template <typename T> __device__ __forceinline__ void load8(const T *p, double *v) {
-  const uint4 r = *(const uint4 *)p;
-  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (double)__uint_as_float(w[e]);
-    const uint4 r2 = *(const uint4 *)(p + 4);
-    const uint32_t w2[4] = {r2.x, r2.y, r2.z, r2.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[4 + e] = (double)__uint_as_float(w2[e]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = (double)half_bits_to_f32<T>(w[e] & 0xFFFFu);
-      v[2 * e + 1] = (double)half_bits_to_f32<T>(w[e] >> 16);
-    }
-  }
-}
 
 // Raw 8-element row chunk (kept undecoded until used, to keep registers low).
 template <typename T> struct Raw8 {
@@ -391,6 +337,44 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
   }
 }
 
+// Per-token group mean (bs = 1, MEAN_GRP_THEN_TOK): one thread per 8-element
+// chunk of an output row, the exact fp64 group sum rounded once as in the
+// block kernels (the mean over one token is the identity), coalesced 16-byte
+// loads and stores.
+template <typename T>
+__global__ __launch_bounds__(256) void pool_grp_kernel(PoolArgs a, int64_t n) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= n) return;
+  const int64_t DC = a.D / 8;
+  const int64_t c = g % DC;
+  const int64_t t = (g / DC) % a.nblk;
+  const int64_t ho = (g / (DC * a.nblk)) % a.Ho;
+  const int64_t b = g / (DC * a.nblk * a.Ho);
+  double s[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = 0.0;
+  if (t < a.l_valid)
+    for (int64_t hh = 0; hh < a.grp; ++hh) {
+      double v[8];
+      load8<T>((const T *)a.x + b * a.sx[0] + (ho * a.grp + hh) * a.sx[1] + t * a.sx[2] + 8 * c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] += v[e];
+    }
+  T r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (T)round_dt<T>(s[e] / (double)a.grp);
+  T *o = (T *)a.out + ((b * a.Ho + ho) * a.nblk + t) * a.D + 8 * c;
+  if (((uintptr_t)o & 15) == 0) {
+    uint4 u[sizeof(T) / 2];
+    __builtin_memcpy(u, r, sizeof(r));
+#pragma unroll
+    for (int q = 0; q < (int)(sizeof(T) / 2); ++q) ((uint4 *)o)[q] = u[q];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = r[e];
+  }
+}
+
 template <typename T, int DC, int BS> static void launch_pool_op(const PoolArgs &a, int64_t nwg, hipStream_t s) {
   switch (a.op) {
     case FBSA_POOL_MEAN_TOK_THEN_GRP:
@@ -434,6 +418,16 @@ int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipS
   a.l_valid = d->l_valid; a.Ho = d->H / d->grp; a.op = d->op;
   for (int k = 0; k < 3; ++k) a.sx[k] = d->sx[k];
   const int64_t nwg = a.B * a.Ho * a.nblk;
+  if (a.bs == 1 && a.op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
+    const int64_t n = nwg * (a.D / 8);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (d->dtype) {
+      case FBSA_BF16: hipLaunchKernelGGL(pool_grp_kernel<bf16>, grid, dim3(256), 0, s, a, n); break;
+      case FBSA_F16: hipLaunchKernelGGL(pool_grp_kernel<f16>, grid, dim3(256), 0, s, a, n); break;
+      default: hipLaunchKernelGGL(pool_grp_kernel<float>, grid, dim3(256), 0, s, a, n); break;
+    }
+    return hip_check(hipGetLastError(), "pool_grp_kernel launch");
+  }
   switch (d->dtype) {
     case FBSA_BF16: launch_pool<bf16>(a, nwg, s); break;
     case FBSA_F16: launch_pool<f16>(a, nwg, s); break;

@@ -15,7 +15,8 @@ MASK_NONE, MASK_SLOT_CAUSAL, MASK_TOKEN_CAUSAL = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 POOL_MEAN_TOK_THEN_GRP, POOL_MEAN_GRP_THEN_TOK, POOL_MAX, POOL_MIN, POOL_MINMAX = 0, 1, 2, 3, 4
 SCORE_DOT, SCORE_MAX2, SCORE_QUEST = 0, 1, 2
-SEL_OWN_FIRST, SEL_SORTED_SINK = 0, 1
+SEL_OWN_FIRST, SEL_SORTED_SINK, SEL_SORTED_TOPK = 0, 1, 2
+QMAX_EXACT = 1
 SEL_CHUNK_SHIFT = 8
 FLAG_OUT_GATE = 1
 
@@ -57,6 +58,17 @@ class SelectDesc(ctypes.Structure):
     ]
 
 
+class QmaxDesc(ctypes.Structure):
+    """Mirror of ``fbsa_qmax_desc``."""
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("convention", ctypes.c_int32), ("sink", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("B", ctypes.c_int64), ("H", ctypes.c_int64), ("nblk", ctypes.c_int64),
+        ("D", ctypes.c_int64), ("tok", ctypes.c_int64), ("la", ctypes.c_int64),
+        ("topk", ctypes.c_int64), ("kk", ctypes.c_int64), ("ncand", ctypes.c_int64),
+    ]
+
+
 _vp = ctypes.c_void_p
 # name -> (restype, argtypes); every symbol declared in include/fbsa.h
 SIGNATURES = {
@@ -73,6 +85,7 @@ SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "fbsa_select_rows": (ctypes.c_int, [ctypes.POINTER(SelectDesc), ctypes.c_int64, ctypes.c_int64,
                                         _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "fbsa_select_qmax": (ctypes.c_int, [ctypes.POINTER(QmaxDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "fbsa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnDesc)]),
     "fbsa_bwd_prep": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 6 + [ctypes.c_size_t, _vp]),
     "fbsa_transpose_index": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, ctypes.c_size_t, _vp]),

@@ -151,7 +151,7 @@ def select_quest(q, k, bs, topk, sink=True, l_valid=None, engine="auto"):
 def _pool_last_token(q, bs, grp):
     """Last token of every query block, averaged over the GQA group:
     ``q.view(B,Hkv,grp,nblk,bs,d).mean(2)[:, :, :, -1, :]``
-    (src/qwen_blocksparse.py:268). A ragged last block's last token is the zero
+    (src/qwen_blocksparse.py:259). A ragged last block's last token is the zero
     padding. Pools the strided view of those tokens with bs = 1."""
     B, Hq, L, D = q.shape
     nblk = (L + bs - 1) // bs
@@ -163,7 +163,7 @@ def _pool_last_token(q, bs, grp):
 
 
 def select_quest_lasttok(q, k, bs, topk, sink=True, engine="auto"):
-    """SelectLastTok (src/qwen_blocksparse.py:256-275): the Quest score of each
+    """SelectLastTok (src/qwen_blocksparse.py:244-264): the Quest score of each
     query block's last token (mean over its GQA group) against the per-block
     key min/max, then ``_finish``. Returns idx (B, Hkv, nblk, kk) int32."""
     Hkv = k.shape[1]
@@ -174,7 +174,7 @@ def select_quest_lasttok(q, k, bs, topk, sink=True, engine="auto"):
 
 
 def select_learned(q, k, Wq, Wk, bs, topk, sink=True, scale=None, minmax=False, engine="auto"):
-    """SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:171-212):
+    """SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:168-213):
     block-pooled q (group mean, then token mean) and k (token mean, or the
     per-block [kmin, kmax]) projected through Wq / Wk (torch matmuls, as the
     reference), then the top-k of scale * sq.sk^T with ``_finish``. A positive
@@ -199,3 +199,74 @@ def select_learned(q, k, Wq, Wk, bs, topk, sink=True, scale=None, minmax=False, 
     return select(sq.contiguous(), sk.contiguous(), score="dot", convention="sorted_sink", topk=topk, sink=sink,
                   engine=engine)
 
+
+
+def select_qmax(a, b1, b2, tok, *, topk, convention="sorted_sink", sink=True, cand=None, engine="auto"):
+    """Row-block max Quest selection (``fbsa_select_qmax``).
+
+    a: (B,H,La,D) query vectors, block i = vectors [i*tok, (i+1)*tok) (vectors
+    at or past La count as zero); b1 = kmax, b2 = kmin (B,H,nblk,D). score(i,j)
+    = max over block i's vectors of rnd(rnd(relu(a).b1_j) + rnd(min(a,0).b2_j))
+    over j <= i, or over row i's entries of ``cand`` (B,H,nblk,M) int32.
+    convention 'sorted_sink' (``_finish``, src/qwen_blocksparse.py:87-99) or
+    'sorted_topk' (the bare ascending top-k set: SelectTwoStage's candidate
+    stage, src/qwen_blocksparse.py:289-290). engine "auto" brackets 16-bit scores
+    on MFMA and computes exactly only what the top-k needs; "fp64" computes
+    every score in float64 -- identical results. Returns int32 (B,H,nblk,kk).
+    """
+    _require_cuda(a, b1, b2)
+    if a.dim() != 4 or b1.dim() != 4 or b1.shape != b2.shape or a.shape[:2] != b1.shape[:2] \
+            or a.shape[3] != b1.shape[3]:
+        raise ValueError("fbsa.select_qmax: a (B,H,La,D), b1/b2 (B,H,nblk,D) expected")
+    if a.dtype != b1.dtype or b2.dtype != a.dtype:
+        raise ValueError("fbsa.select_qmax: operands must share a dtype")
+    B, H, La, D = a.shape
+    nblk = b1.shape[2]
+    a, b1, b2 = a.contiguous(), b1.contiguous(), b2.contiguous()
+    d = _lib.QmaxDesc()
+    d.dtype = _dtype_code(a)
+    d.convention = {"sorted_sink": _lib.SEL_SORTED_SINK, "sorted_topk": _lib.SEL_SORTED_TOPK}[convention]
+    d.sink = 1 if (sink and convention == "sorted_sink") else 0
+    d.flags = _lib.QMAX_EXACT if engine == "fp64" else 0
+    k_eff = min(topk, nblk)
+    kk = k_eff + 1 + d.sink if convention == "sorted_sink" else k_eff
+    d.B, d.H, d.nblk, d.D, d.tok, d.la, d.topk, d.kk = B, H, nblk, D, tok, La, topk, kk
+    if cand is not None:
+        _require_cuda(cand)
+        if cand.dim() != 4 or cand.shape[:3] != (B, H, nblk) or cand.dtype != torch.int32:
+            raise ValueError(f"fbsa.select_qmax: cand must be int32 {(B, H, nblk)} + (M,)")
+        cand = cand.contiguous()
+        d.ncand = cand.shape[3]
+    sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
+    _lib.check(_lib.load().fbsa_select_qmax(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(cand), _ptr(sel), _stream()),
+               "fbsa_select_qmax")
+    return sel
+
+
+def select_quest_qmax(q, k, bs, topk, sink=True, engine="auto"):
+    """SelectMaxQMax (src/qwen_blocksparse.py:216-241): the Quest score maxed
+    over each query block's tokens (each token first averaged over its GQA
+    group, rounded) against the per-block key min/max, then ``_finish``. The
+    reference loops over query blocks; here one kernel scores every block.
+    Returns idx (B, Hkv, nblk, kk) int32."""
+    Hkv = k.shape[1]
+    grp = q.shape[1] // Hkv
+    qg = pool(q, 1, "mean_grp_then_tok", grp=grp)
+    kmin, kmax = pool(k, bs, "minmax")
+    return select_qmax(qg, kmax, kmin, bs, topk=topk, sink=sink, engine=engine)
+
+
+def select_two_stage(q, k, bs, topk, sink=True, over=4, engine="auto"):
+    """SelectTwoStage (src/qwen_blocksparse.py:267-299): candidates = the top
+    M = min(over*topk, nblk) blocks by the block-mean Quest score (the
+    SelectMax score), then the token-max Quest score over the candidates
+    only, then ``_finish``. Returns idx (B, Hkv, nblk, kk) int32."""
+    Hkv = k.shape[1]
+    grp = q.shape[1] // Hkv
+    qg = pool(q, 1, "mean_grp_then_tok", grp=grp)
+    qpool = pool(qg, bs, "mean_tok_then_grp", grp=1)
+    kmin, kmax = pool(k, bs, "minmax")
+    nblk = kmax.shape[2]
+    m = min(over * topk, nblk)
+    cand = select_qmax(qpool, kmax, kmin, 1, topk=m, convention="sorted_topk", engine=engine)
+    return select_qmax(qg, kmax, kmin, bs, topk=topk, sink=sink, cand=cand, engine=engine)

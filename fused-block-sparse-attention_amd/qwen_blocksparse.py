@@ -15,9 +15,12 @@ Same surface as ``src/qwen_blocksparse.py``:
   ``out_gate`` (B, Hq, L, d) applies ``o * sigmoid(out_gate)`` in the
   kernel's epilogue (the Qwen output gate, ``src/patch_qwen.py:55``).
 * ``SelectMax`` (``:102-121``): Quest min/max upper-bound selector on the
-  pooling and streaming top-k kernels; ``SelectLastTok`` (``:256-275``, the
-  same score from each block's last token); ``SelectLearned`` /
-  ``SelectLearnedMinMax`` (``:171-212``, pooled features through Wq / Wk, the
+  pooling and streaming top-k kernels; ``SelectLastTok`` (``:244-264``, the
+  same score from each block's last token); ``SelectMaxQMax`` /
+  ``SelectTwoStage`` (``:216-241``, ``:267-299``, the score maxed over each
+  block's tokens, over all blocks or over block-mean candidates, on the
+  row-block max kernel); ``SelectLearned`` /
+  ``SelectLearnedMinMax`` (``:168-213``, pooled features through Wq / Wk, the
   projections in torch as in the reference); ``SelectAll`` (``:155-165``).
 * ``block_mass`` -- the true block mass ``SelectOracle`` selects from (the
   ``capture_mass`` loop of ``src/eval_qwen_ppl.py:84-95``) on a fused kernel.
@@ -113,7 +116,7 @@ class SelectMax:
 
 class SelectLastTok:
     """SelectMax scored by each query block's last token (its GQA-group mean)
-    instead of the block mean (``src/qwen_blocksparse.py:256-275``); pooling and
+    instead of the block mean (``src/qwen_blocksparse.py:244-264``); pooling and
     the streaming top-k run on the GPU kernels."""
 
     def __init__(self, topk, bs, sink=True):
@@ -124,9 +127,38 @@ class SelectLastTok:
         return selection.select_quest_lasttok(q, k, self.bs, self.topk, sink=self.sink).long()
 
 
+class SelectMaxQMax:
+    """SelectMax with the Quest score maxed over the query block's tokens
+    instead of scored on their mean: score(i, j) = max_t relu(q_t) . kmax_j +
+    min(q_t, 0) . kmin_j, q_t the GQA-group mean of token t
+    (``src/qwen_blocksparse.py:216-241``). One kernel scores every query block
+    (brackets on the matrix cores, exact float64 where the top-k needs it)
+    instead of the reference's loop over blocks."""
+
+    def __init__(self, topk, bs, sink=True):
+        self.topk, self.bs, self.sink = topk, bs, sink
+
+    @torch.no_grad()
+    def select(self, q, k):
+        return selection.select_quest_qmax(q, k, self.bs, self.topk, sink=self.sink).long()
+
+
+class SelectTwoStage:
+    """Two-stage Quest selection (``src/qwen_blocksparse.py:267-299``): the
+    block-mean score picks over * topk candidates, the token-max score
+    re-ranks them, then top-k causal + own (+ sink), sorted."""
+
+    def __init__(self, topk, bs, sink=True, over=4):
+        self.topk, self.bs, self.sink, self.over = topk, bs, sink, over
+
+    @torch.no_grad()
+    def select(self, q, k):
+        return selection.select_two_stage(q, k, self.bs, self.topk, sink=self.sink, over=self.over).long()
+
+
 class SelectLearned:
     """Learned selector: block-pooled q / k projected through Wq / Wk (d, sel_dim),
-    top-k of scale * sq.sk^T (``src/qwen_blocksparse.py:171-189``)."""
+    top-k of scale * sq.sk^T (``src/qwen_blocksparse.py:168-187``)."""
 
     def __init__(self, Wq, Wk, topk, bs, sink=True, scale=None):
         self.Wq, self.Wk = Wq, Wk
@@ -141,7 +173,7 @@ class SelectLearned:
 
 class SelectLearnedMinMax(SelectLearned):
     """SelectLearned with the per-block key [kmin, kmax] (2d features) through Wk
-    (2d, sel_dim) instead of the key mean (``src/qwen_blocksparse.py:192-212``)."""
+    (2d, sel_dim) instead of the key mean (``src/qwen_blocksparse.py:190-213``)."""
 
     @torch.no_grad()
     def select(self, q, k):

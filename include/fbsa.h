@@ -132,8 +132,12 @@ enum { FBSA_SCORE_DOT = 0, FBSA_SCORE_MAX2 = 1, FBSA_SCORE_QUEST = 2 };
  *              (src/ssa_model.py:151-165)
  * SORTED_SINK: _finish: top-k over j <= i (own included), non-finite picks
  *              -> i, + own (+ sink block 0), sorted ascending
- *              (src/qwen_blocksparse.py:87-99) */
-enum { FBSA_SEL_OWN_FIRST = 0, FBSA_SEL_SORTED_SINK = 1 };
+ *              (src/qwen_blocksparse.py:87-99)
+ * SORTED_TOPK: the top-k set of SORTED_SINK alone (non-finite picks -> i,
+ *              ascending, no own or sink appended): the candidate stage
+ *              cand = s1.topk(M) of SelectTwoStage, used as a set
+ *              (src/qwen_blocksparse.py:289-290). fbsa_select_qmax only. */
+enum { FBSA_SEL_OWN_FIRST = 0, FBSA_SEL_SORTED_SINK = 1, FBSA_SEL_SORTED_TOPK = 2 };
 
 /* fbsa_select_desc.flags: bits 8..23 = candidate tiles (64 key blocks each)
  * per workgroup of the MFMA path, 0 = chosen from the sizes. Tuning and tests
@@ -167,6 +171,36 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
 int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a,
                      const void *b1, const void *b2, int32_t *sel, float *sel_score, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* Row-block max Quest selection. The score of query block i and key block j
+ * is the best Quest score over the tok query vectors of block i:
+ *   score(i, j) = max_t rnd(rnd(relu(a_t).b1_j) + rnd(min(a_t,0).b2_j))
+ * (b1 = per-block key max, b2 = key min; rnd as for FBSA_SCORE_QUEST), over
+ * the key blocks j <= i or, when cand != NULL, over row i's entries of cand
+ * (B,H,nblk,ncand) int32 (each row ascending, as SORTED_TOPK writes it;
+ * repeats and entries outside [0, i] are skipped). Then the top-k of the
+ * convention (SORTED_SINK or SORTED_TOPK), ties to the lower block index.
+ * a: (B,H,la,D) contiguous query vectors, block i = vectors [i*tok,
+ * (i+1)*tok), vectors at or past la are zero (the reference's zero padding);
+ * b1, b2: (B,H,nblk,D) contiguous; sel: (B,H,nblk,kk). Operands are finite.
+ * 16-bit operands with tok 64 or 128 bracket the scores on MFMA and compute
+ * exactly (float64) only the scores the top-k needs; other cases, or
+ * FBSA_QMAX_EXACT, compute every score in float64; both give the same
+ * result. Supports D in {32,64,128,256}, nblk <= 65536 and at most 4096
+ * columns per row (nblk, or ncand with a candidate list). Replaces
+ * SelectMaxQMax.select (tok = bs, a = the GQA-group mean of every token;
+ * src/qwen_blocksparse.py:216-241) and both stages of SelectTwoStage
+ * (tok = 1 on the pooled query for the candidates, then tok = bs over them;
+ * src/qwen_blocksparse.py:267-299). */
+enum { FBSA_QMAX_EXACT = 1 };
+
+typedef struct fbsa_qmax_desc {
+  int32_t dtype, convention, sink, flags;
+  int64_t B, H, nblk, D, tok, la, topk, kk, ncand;
+} fbsa_qmax_desc;
+
+int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2,
+                     const int32_t *cand, int32_t *sel, void *stream);
 
 /* ---- backward -------------------------------------------------------- */
 

@@ -9,13 +9,16 @@ Restates, in numpy, the reference's block-pair selection:
   (``src/qwen_blocksparse.py:111-116``).
 * ``pool_tok`` -- ``BlockSparseSSA._scores`` pooling (``src/ssa_model.py:114-117``).
 * ``pool_last_token_grp`` / ``pool_mean_tok`` -- the ``SelectLastTok`` and
-  ``SelectLearned`` poolings (``src/qwen_blocksparse.py:268``, ``:181-182``).
+  ``SelectLearned`` poolings (``src/qwen_blocksparse.py:259``, ``:183``).
 * ``scores`` -- the nblk x nblk contraction: plain dot (``src/scale_sel.py:33``),
   max of two dots (``src/ssa_model.py:118-119``), Quest q+/q- split
   (``src/qwen_blocksparse.py:117-120``), each rounded where torch rounds.
 * ``select_conv_a`` -- own block first + top-k content blocks
   (``src/ssa_model.py:151-165``; ``src/bench_crossover.py:41-54``).
 * ``select_conv_b`` -- ``_finish`` (``src/qwen_blocksparse.py:87-99``).
+* ``pool_grp_mean_tok`` / ``scores_qmax`` / ``select_topk_set`` -- the
+  token-max Quest score of ``SelectMaxQMax`` and the two stages of
+  ``SelectTwoStage`` (``src/qwen_blocksparse.py:216-241``, ``:267-299``).
 
 Tie-break: candidates are ranked NaN first (torch.topk treats NaN as the
 largest value), then by descending score, then by ascending block index.
@@ -76,7 +79,7 @@ def pool_last_token_grp(q, hkv, bs, dtype):
     """(B,Hq,N,D) -> (B,Hkv,nblk,D): the GQA-group mean (rounded) of each
     block's last token; a ragged last block's last token is the zero padding.
     ``q.view(B,Hkv,grp,nblk,bs,d).mean(2)[:, :, :, -1, :]``
-    (``src/qwen_blocksparse.py:268``)."""
+    (``src/qwen_blocksparse.py:259``)."""
     q = np.asarray(q, dtype=np.float64)
     B, Hq, N, D = q.shape
     grp = Hq // hkv
@@ -87,7 +90,7 @@ def pool_last_token_grp(q, hkv, bs, dtype):
 
 def pool_mean_tok(x, bs, dtype):
     """(B,H,N,D) -> (B,H,nblk,D): per-head token mean (rounded), zero padding
-    counted: ``kp.view(B,Hkv,nblk,bs,d).mean(3)`` (``src/qwen_blocksparse.py:182``)."""
+    counted: ``kp.view(B,Hkv,nblk,bs,d).mean(3)`` (``src/qwen_blocksparse.py:183``)."""
     x = np.asarray(x, dtype=np.float64)
     B, H, N, D = x.shape
     x, nblk = _pad_tokens(x, bs, 2)
@@ -238,7 +241,7 @@ def select_quest(q, k, bs, topk, sink, dtype):
 
 
 def select_quest_lasttok(q, k, bs, topk, sink, dtype):
-    """``SelectLastTok.select`` (``src/qwen_blocksparse.py:262-275``): Quest
+    """``SelectLastTok.select`` (``src/qwen_blocksparse.py:244-264``): Quest
     scores of each block's last-token group mean, then ``_finish``."""
     hkv = k.shape[1]
     qlast = pool_last_token_grp(q, hkv, bs, dtype)
@@ -249,12 +252,82 @@ def select_quest_lasttok(q, k, bs, topk, sink, dtype):
 
 def select_learned_features(sq, sk, topk, sink, dtype, scale):
     """``SelectLearned`` / ``SelectLearnedMinMax`` from their projected features
-    (``src/qwen_blocksparse.py:185-189``, ``:208-212``): score =
+    (``src/qwen_blocksparse.py:184-187``, ``:210-213``): score =
     rnd(scale * rnd(sq . sk)) in the feature dtype, then ``_finish``. Returns
     (idx, score, unscaled rnd(sq . sk))."""
     raw = scores(sq, sk, dtype, "dot")
     sc = round_to(scale * raw, dtype)
     return select_conv_b(sc, topk, sink), sc, raw
+
+
+def pool_grp_mean_tok(q, hkv, dtype):
+    """(B,Hq,N,D) -> (B,Hkv,N,D): the GQA-group mean of every token (rounded),
+    ``qp.view(B,Hkv,grp,nblk,bs,d).mean(2)`` (``src/qwen_blocksparse.py:231``,
+    ``:281``) before the block padding (padding tokens are zeros)."""
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, N, D = q.shape
+    grp = Hq // hkv
+    return round_to(q.reshape(B, hkv, grp, N, D).sum(axis=2) / grp, dtype)
+
+
+def scores_qmax(qg, kmax, kmin, bs, dtype, cand=None):
+    """Row-block max Quest scores (B,H,nblk,nblk): score(i,j) = max over the bs
+    tokens t of block i (zero padded) of rnd(rnd(relu(q_t).kmax_j) +
+    rnd(min(q_t,0).kmin_j)) -- the per-block loop of ``SelectMaxQMax``
+    (``src/qwen_blocksparse.py:236-240``). With ``cand`` (B,H,nblk,M) only the
+    candidate columns keep their score and every other entry is -inf (the
+    scatter into a -inf matrix of ``SelectTwoStage``, ``:297-298``)."""
+    qg, nblk = _pad_tokens(np.asarray(qg, dtype=np.float64), bs, 2)
+    B, H, _, D = qg.shape
+    tok = scores(qg, kmax, dtype, "quest", b2=kmin)              # (B,H,nblk*bs,nblk)
+    sc = tok.reshape(B, H, nblk, bs, -1).max(axis=3)
+    if cand is not None:
+        keep = np.zeros(sc.shape, dtype=bool)
+        np.put_along_axis(keep, np.asarray(cand, dtype=np.int64), True, axis=-1)
+        sc = np.where(keep, sc, -np.inf)
+    return sc
+
+
+def select_topk_set(score, topk):
+    """Candidate stage of ``SelectTwoStage`` (``src/qwen_blocksparse.py:288-290``):
+    the top min(topk, nblk) blocks over j <= i (future blocks are -inf), used
+    as a set -- non-finite picks become the own block (a -inf pick is a future
+    block, which the final ``_finish`` masks anyway), sorted ascending, nothing
+    appended. score: (B,H,R,nblk); returns (B,H,R,min(topk,nblk)) int64."""
+    score = np.asarray(score, dtype=np.float64)
+    B, H, R, nblk = score.shape
+    rows = np.arange(R)
+    masked = np.where(np.arange(nblk)[None, :] > rows[:, None], -np.inf, score)
+    kk_t = min(topk, nblk)
+    order = _rank(masked, np.ones_like(masked, dtype=bool))[..., :kk_t]
+    vals = np.take_along_axis(masked, order, axis=-1)
+    own = np.broadcast_to(rows[None, None, :, None], order.shape)
+    return np.sort(np.where(np.isfinite(vals), order, own), axis=-1).astype(np.int64)
+
+
+def select_quest_qmax(q, k, bs, topk, sink, dtype):
+    """``SelectMaxQMax.select`` (``src/qwen_blocksparse.py:216-241``).
+    Returns (idx (B,Hkv,nblk,kk) int64, score (B,Hkv,nblk,nblk))."""
+    hkv = k.shape[1]
+    qg = pool_grp_mean_tok(q, hkv, dtype)
+    kmin, kmax = pool_minmax(k, bs)
+    sc = scores_qmax(qg, kmax, kmin, bs, dtype)
+    return select_conv_b(sc, topk, sink), sc
+
+
+def select_two_stage(q, k, bs, topk, sink, over, dtype):
+    """``SelectTwoStage.select`` (``src/qwen_blocksparse.py:267-299``): block-mean
+    Quest scores pick M = min(over*topk, nblk) candidates, the token-max Quest
+    score re-ranks them, then ``_finish``. Returns (idx, final scores, cand)."""
+    hkv = k.shape[1]
+    qg = pool_grp_mean_tok(q, hkv, dtype)
+    qpool = pool_mean_tok(qg, bs, dtype)                      # qg.mean(3), :284
+    kmin, kmax = pool_minmax(k, bs)
+    nblk = kmax.shape[2]
+    s1 = scores(qpool, kmax, dtype, "quest", b2=kmin)
+    cand = select_topk_set(s1, min(over * topk, nblk))
+    s2 = scores_qmax(qg, kmax, kmin, bs, dtype, cand=cand)
+    return select_conv_b(s2, topk, sink), s2, cand
 
 
 def near_tie_rows(score, sel_valid_sets, k_eff, valid_mask, rel=1e-6):

@@ -255,7 +255,7 @@ def test_qwen_selectmax_forward_matches_oracle_with_outgate(dtype):
 
 @pytest.mark.parametrize("L,d,dtype", [(2048, 64, "bf16"), (2000, 128, "bf16"), (1024, 64, "f32")])
 def test_qwen_select_lasttok_matches_oracle(L, d, dtype):
-    # SelectLastTok (src/qwen_blocksparse.py:256-275): Quest score of each block's
+    # SelectLastTok (src/qwen_blocksparse.py:244-264): Quest score of each block's
     # last-token group mean; the ragged block's last token is zero padding
     from qwen_blocksparse import SelectLastTok
     g = torch.Generator().manual_seed(21)
@@ -270,7 +270,7 @@ def test_qwen_select_lasttok_matches_oracle(L, d, dtype):
 @pytest.mark.parametrize("minmax", [False, True])
 @pytest.mark.parametrize("sel_dim,dtype", [(64, "bf16"), (32, "bf16"), (64, "f32")])
 def test_qwen_select_learned_matches_oracle(minmax, sel_dim, dtype):
-    # SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:171-212): pooled
+    # SelectLearned / SelectLearnedMinMax (src/qwen_blocksparse.py:168-213): pooled
     # features (checked against the oracle's pools) projected by torch as in the
     # reference, then the streaming top-k of scale * sq.sk^T. With sel_dim 64 the
     # default scale is 1/8 (exact); with 32 it rounds, and may merge neighbouring
@@ -324,7 +324,7 @@ def test_qwen_block_mass_matches_oracle(dtype, L, d, bs):
     np.testing.assert_allclose(m.sum(-1), 1.0, atol=1e-4)
     np.testing.assert_allclose(m, ref, atol=5e-5)
     assert np.abs(m - ref).mean() < 2e-6
-    # SelectOracle on it (src/qwen_blocksparse.py:124-138)
+    # SelectOracle on it (src/qwen_blocksparse.py:124-137)
     topk = 3
     idx = SelectOracle(topk=topk, bs=bs, sink=True, mass=got).select(None, None).cpu().numpy()
     ridx = osel.select_conv_b(ref, topk, True)

@@ -68,7 +68,7 @@ def test_pool_mean_matches_torch_cpu(dtype):
 
 @pytest.mark.parametrize("N", [512, 500])
 def test_pool_last_token_and_token_mean_match_torch_cpu(N):
-    # the reference's expressions (src/qwen_blocksparse.py:268, :182) on the same bf16 data
+    # the reference's expressions (src/qwen_blocksparse.py:259, :183) on the same bf16 data
     B, Hq, Hkv, D, bs = 2, 4, 2, 32, 64
     g = torch.Generator().manual_seed(5)
     q = torch.randn(B, Hq, N, D, generator=g).to(torch.bfloat16)
@@ -245,3 +245,114 @@ def test_near_tie_census():
     assert not osel.near_tie_rows(score, np.array([[[0, 4]]]), 2, valid)[0, 0]
     score2 = np.array([[[5.0, 3.0, 2.5, 1.0, 2.0]]])
     assert not osel.near_tie_rows(score2, np.array([[[0, 1]]]), 2, valid)[0, 0]
+
+
+# ---------------------------------------------------------------- token-max Quest (SelectMaxQMax / SelectTwoStage)
+def _torch_token_max_parts(q, k, bs):
+    """Padded per-token group means and per-block key extremes, as the
+    reference forms them (src/qwen_blocksparse.py:228-234, :278-283)."""
+    B, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    nblk = (L + bs - 1) // bs
+    qp = torch.nn.functional.pad(q, (0, 0, 0, nblk * bs - L))
+    kp = torch.nn.functional.pad(k, (0, 0, 0, nblk * bs - L))
+    qg = qp.view(B, Hkv, Hq // Hkv, nblk, bs, D).mean(2)
+    kb = kp.view(B, Hkv, nblk, bs, D)
+    return qg, kb.min(3).values, kb.max(3).values, nblk
+
+
+def _torch_qmax_scores(qg, kmin, kmax):
+    # the per-query-block loop of SelectMaxQMax (src/qwen_blocksparse.py:235-240) on the CPU
+    B, H, nblk = kmin.shape[:3]
+    score = torch.empty(B, H, nblk, nblk)
+    for i in range(nblk):
+        qi = qg[:, :, i]
+        s = (torch.einsum("bhtd,bhjd->bhtj", qi.clamp(min=0), kmax)
+             + torch.einsum("bhtd,bhjd->bhtj", qi.clamp(max=0), kmin))
+        score[:, :, i] = s.max(2).values
+    return score
+
+
+def _torch_finish(score, topk, sink):
+    B, H, nblk, _ = score.shape
+    ar = torch.arange(nblk)
+    sc = score.masked_fill(ar.view(1, 1, nblk, 1) < ar.view(1, 1, 1, nblk), float("-inf"))
+    tv, ti = sc.topk(min(topk, nblk), dim=-1)
+    own = ar.view(1, 1, nblk, 1).expand(B, H, nblk, 1)
+    ti = torch.where(torch.isfinite(tv), ti, own.expand_as(ti))
+    parts = [ti, own] + ([torch.zeros(B, H, nblk, 1, dtype=torch.long)] if sink else [])
+    return torch.cat(parts, -1).sort(-1).values.numpy()
+
+
+@pytest.mark.parametrize("L", [512, 470])
+def test_qmax_scores_match_reference_loop_torch_cpu(L):
+    B, Hq, Hkv, D, bs = 1, 4, 2, 32, 64
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, Hq, L, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16)
+    qg, kmin, kmax, nblk = _torch_token_max_parts(q, k, bs)
+    ref = _torch_qmax_scores(qg, kmin, kmax).double().numpy()
+    idx, sc = osel.select_quest_qmax(q.double().numpy(), k.double().numpy(), bs, 3, True, "bf16")
+    # torch's CPU accumulator may round a token's score differently at a bf16
+    # midpoint: at most one ulp, rarely
+    diff = sc != ref
+    assert diff.mean() < 5e-3
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(ref[diff]))) - 7)
+    assert np.all(np.abs(sc[diff] - ref[diff]) <= ulp)
+    if L % bs:
+        assert np.all(sc[:, :, -1] >= 0)  # padding tokens score 0 and take part in the max
+    assert idx.shape == (B, Hkv, nblk, 5)
+
+
+@pytest.mark.parametrize("over", [1, 2, 4])
+def test_qmax_and_two_stage_match_reference_torch_cpu_fp32(over):
+    # fp32 data (no exact ties): the whole selection equals the reference's
+    # algorithm run by torch on the CPU, gather/scatter of the candidates included
+    B, Hq, Hkv, L, D, bs, topk = 1, 4, 2, 24 * 32, 16, 32, 4
+    g = torch.Generator().manual_seed(12)
+    q, k = torch.randn(B, Hq, L, D, generator=g), torch.randn(B, Hkv, L, D, generator=g)
+    qg, kmin, kmax, nblk = _torch_token_max_parts(q, k, bs)
+    ref_qmax = _torch_finish(_torch_qmax_scores(qg, kmin, kmax), topk, True)
+    got_qmax, _ = osel.select_quest_qmax(q.numpy(), k.numpy(), bs, topk, True, "f32")
+    np.testing.assert_array_equal(got_qmax, ref_qmax)
+    # SelectTwoStage (src/qwen_blocksparse.py:284-299)
+    qpool = qg.mean(3)
+    s1 = (torch.einsum("bhid,bhjd->bhij", qpool.clamp(min=0), kmax)
+          + torch.einsum("bhid,bhjd->bhij", qpool.clamp(max=0), kmin))
+    diag = torch.arange(nblk)
+    s1 = s1.masked_fill(diag.view(1, 1, nblk, 1) < diag.view(1, 1, 1, nblk), float("-inf"))
+    M = min(over * topk, nblk)
+    cand = s1.topk(M, dim=-1).indices
+    ci = cand.unsqueeze(-1).expand(B, Hkv, nblk, M, D)
+    kmax_c = torch.gather(kmax.unsqueeze(2).expand(B, Hkv, nblk, nblk, D), 3, ci)
+    kmin_c = torch.gather(kmin.unsqueeze(2).expand(B, Hkv, nblk, nblk, D), 3, ci)
+    s2 = (torch.einsum("bhitd,bhimd->bhitm", qg.clamp(min=0), kmax_c)
+          + torch.einsum("bhitd,bhimd->bhitm", qg.clamp(max=0), kmin_c)).max(3).values
+    full = torch.full((B, Hkv, nblk, nblk), float("-inf")).scatter_(3, cand, s2)
+    ref_two = _torch_finish(full, topk, True)
+    got_two, _, got_cand = osel.select_two_stage(q.numpy(), k.numpy(), bs, topk, True, over, "f32")
+    np.testing.assert_array_equal(got_two, ref_two)
+    past = [set(r[r <= i].tolist()) for i, r in enumerate(cand[0, 0].numpy())]
+    assert [set(r.tolist()) for r in got_cand[0, 0]] == [p | ({i} if len(p) < M else set()) for i, p in enumerate(past)]
+
+
+def test_qmax_closed_forms():
+    # tokens constant within each block: the token max is the block mean, so
+    # SelectMaxQMax reduces to SelectMax; candidates covering every block make
+    # SelectTwoStage reduce to SelectMaxQMax
+    B, Hq, Hkv, D, bs, nblk = 1, 4, 2, 32, 32, 20
+    c = on.round_bf16(RNG.standard_normal((B, Hq, nblk, 1, D)))
+    q = np.broadcast_to(c, (B, Hq, nblk, bs, D)).reshape(B, Hq, nblk * bs, D)
+    k = on.round_bf16(RNG.standard_normal((B, Hkv, nblk * bs, D)))
+    for topk, sink in ((3, True), (5, False), (25, True)):
+        iq, sq = osel.select_quest_qmax(q, k, bs, topk, sink, "bf16")
+        im, sm = osel.select_quest(q, k, bs, topk, sink, "bf16")
+        np.testing.assert_array_equal(sq, sm)
+        np.testing.assert_array_equal(iq, im)
+    q2 = on.round_bf16(RNG.standard_normal((B, Hq, nblk * bs, D)))
+    iq2, sq2 = osel.select_quest_qmax(q2, k, bs, 4, True, "bf16")
+    i2, s2, cand = osel.select_two_stage(q2, k, bs, 4, True, 5, "bf16")
+    np.testing.assert_array_equal(i2, iq2)
+    fut = np.arange(nblk)[None, :] > np.arange(nblk)[:, None]
+    np.testing.assert_array_equal(np.where(fut, -np.inf, s2), np.where(fut, -np.inf, sq2))
+    assert all(set(cand[0, 0, i].tolist()) == set(range(i + 1)) for i in range(nblk))
