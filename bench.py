@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--splits", type=int, default=4, help="row ranges of the overlapped step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-rows", type=int, default=4096, help="query blocks in the CPU sample (4096 = all at config 3)")
+    p.add_argument("--qwen", choices=["max", "qmax", "twostage", "lasttok"], default=None,
+                   help="time configuration 4 instead (GQA Qwen shape) with this qwen_blocksparse selector")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     return p.parse_args()
@@ -142,6 +144,100 @@ def cpu_baseline(q, k, v, bs, topk, rows_wanted):
     }
 
 
+def rope_partial(x, dims=64, theta=1e7):
+    """rotate_half rotary embedding on the first `dims` channels at positions
+    0..N-1 (Qwen's partial RoPE, applied by the caller before attention)."""
+    import torch
+    N = x.shape[2]
+    half = dims // 2
+    inv = 1.0 / theta ** (torch.arange(0, dims, 2, device=x.device, dtype=torch.float32) / dims)
+    ang = torch.arange(N, device=x.device, dtype=torch.float32)[:, None] * inv[None]
+    cos, sin = torch.cat([ang.cos()] * 2, -1), torch.cat([ang.sin()] * 2, -1)
+    xr = x[..., :dims].float()
+    rot = torch.cat([-xr[..., half:], xr[..., :half]], -1)
+    return torch.cat([(xr * cos + rot * sin).to(x.dtype), x[..., dims:]], -1)
+
+
+def qwen_main(a):
+    """Configuration 4: B1 N65536 Hq16 Hkv2 D256, block
+    128 (nblk 512), post-RoPE q/k, convention B top-32 + own + sink per KV
+    head, output gate sigmoid(g). One step = selector.select(q, k) and the
+    fused GQA forward with the gate epilogue (qwen_blocksparse drop-ins)."""
+    import torch
+    import qwen_blocksparse as qb
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    B, Hq, Hkv, N, D, bs, topk = 1, 16, 2, 65536, 256, 128, 32
+    nblk = N // bs
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = rope_partial((torch.randn(B, Hq, N, D, generator=g, device=dev)).to(torch.bfloat16))
+    k = rope_partial((torch.randn(B, Hkv, N, D, generator=g, device=dev)).to(torch.bfloat16))
+    v = torch.randn(B, Hkv, N, D, generator=g, device=dev).to(torch.bfloat16)
+    og = torch.randn(B, Hq, N, D, generator=g, device=dev).to(torch.bfloat16)
+    S = {"max": qb.SelectMax, "qmax": qb.SelectMaxQMax, "twostage": qb.SelectTwoStage,
+         "lasttok": qb.SelectLastTok}[a.qwen](topk=topk, bs=bs, sink=True)
+    stream = torch.cuda.current_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    def step():
+        return qb.blocksparse_forward(q, k, v, selector=S, topk=topk, bs=bs, out_gate=og)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / a.steps
+    # per-stage times: the selector alone, then the forward on its indices
+    sel_ev, fwd_ev = [], []
+    for it in range(a.warmup + a.steps):
+        e0, e1, e2 = ev(), ev(), ev()
+        e0.record(stream)
+        idx = S.select(q, k)
+        e1.record(stream)
+        qb.blocksparse_forward(q, k, v, selector=_Fixed(idx), topk=topk, bs=bs, out_gate=og)
+        e2.record(stream)
+        if it >= a.warmup:
+            sel_ev.append((e0, e1))
+            fwd_ev.append((e1, e2))
+    torch.cuda.synchronize()
+    t_sel = sum(x.elapsed_time(y) for x, y in sel_ev) / a.steps
+    t_fwd = sum(x.elapsed_time(y) for x, y in fwd_ev) / a.steps
+    kk = topk + 2
+    flops = 4.0 * B * Hq * nblk * kk * bs * bs * D
+    achieved = flops / (t_fwd * 1e-3) / 1e12
+    out = {
+        "metric": f"select+fwd tokens/s at {N // 1000}k tokens, 1 GPU (bf16, GQA Hq{Hq} Hkv{Hkv} D{D} bs{bs} "
+                  f"top-{topk} +own +sink, {type(S).__name__})",
+        "value": B * N / (ms_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (q,k,v,g ~ N(0,1), RoPE on q/k dims 0..63, theta 1e7, seed 0, device generator)",
+        "config": {"workload": f"BASELINE configs[3]: qwen_blocksparse.{type(S).__name__} + blocksparse_forward "
+                               "with the output gate", "B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": D, "block": bs,
+                   "nblk": nblk, "topk": topk, "kk": kk},
+        "ms_select": t_sel, "ms_fwd": t_fwd,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "fbsa::fwd_kernel<bf16,128,256>", "flop_per_launch": flops},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+class _Fixed:
+    """Selector returning precomputed indices (separates the stage timings)."""
+
+    def __init__(self, idx):
+        self.idx = idx
+
+    def select(self, q, k):
+        return self.idx
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -150,6 +246,9 @@ def main():
         sys.exit(2)
     if a.calibrate_copy:
         calibrate_copy()
+        return
+    if a.qwen:
+        qwen_main(a)
         return
     import torch
     from fbsa_amd import ops, pipeline, selection

@@ -185,8 +185,10 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
   return run_select(d, row_begin, row_end, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
 }
 
+size_t fbsa_select_qmax_workspace_bytes(const fbsa_qmax_desc *d) { return d ? select_qmax_workspace_bytes(d) : 0; }
+
 int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2, const int32_t *cand,
-                     int32_t *sel, void *stream) {
+                     int32_t *sel, void *workspace, size_t workspace_bytes, void *stream) {
   if (!d) return fail(FBSA_EINVAL, "fbsa_select_qmax: null descriptor");
   if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_select_qmax: bad dtype %d", d->dtype);
   if (d->convention != FBSA_SEL_SORTED_SINK && d->convention != FBSA_SEL_SORTED_TOPK)
@@ -211,7 +213,11 @@ int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, con
   if (!aligned(a, 16) || !aligned(b1, 16) || !aligned(b2, 16) || !aligned(sel, 4) || (cand && !aligned(cand, 4)))
     return fail(FBSA_EINVAL, "fbsa_select_qmax: misaligned pointer (a, b1, b2 need 16 bytes)");
   if (d->B * d->H * d->nblk > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: grid too large");
-  return run_select_qmax(d, a, b1, b2, cand, sel, (hipStream_t)stream);
+  // the workspace enables the MFMA engine; without one every score is float64 (same result)
+  const size_t need = select_qmax_workspace_bytes(d);
+  void *ws = (workspace && need > 0 && workspace_bytes >= need) ? workspace : nullptr;
+  if (ws && !aligned(ws, 16)) return fail(FBSA_EINVAL, "fbsa_select_qmax: workspace must be 16-byte aligned");
+  return run_select_qmax(d, a, b1, b2, cand, sel, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -29,8 +29,9 @@ int run_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float 
 size_t select_workspace_bytes(const fbsa_select_desc *d);
 int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *a, const void *b1, const void *b2,
                int32_t *sel, float *sel_score, void *ws, hipStream_t s);
+size_t select_qmax_workspace_bytes(const fbsa_qmax_desc *d);
 int run_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2, const int32_t *cand,
-                    int32_t *sel, hipStream_t s);
+                    int32_t *sel, void *ws, hipStream_t s);
 
 // ---- backward ----
 // Byte offsets of the backward workspace regions (each 256-byte aligned).

@@ -11,35 +11,41 @@
 // (non-finite picks -> own block, + own, + sink, ascending) or, for a
 // candidate stage, as the bare ascending top-k set.
 //
-// One workgroup per (b, h, query block i), larger i first (the rows with the
-// most columns start early). Two 32-bit orderable keys per column live in
-// LDS.
+// One workgroup (four waves) per (b, h, query block i), larger i first (the
+// rows with the most columns start early). Two 32-bit orderable keys per
+// column live in LDS.
 //  1. Brackets (16-bit operands, 64 or 128 query vectors per block, D in
-//     {32, 64, 128, 256}): each of the four waves holds tok/64 tiles of 16
-//     query vectors, split into their positive and negative parts, as MFMA A
-//     operands for the whole row. For each tile of 16 columns the key max/min
-//     rows go straight from global memory (L2) into B operands and the two
-//     dot products of every (vector, column) pair come from bf16/f16 MFMA
-//     with fp32 accumulation. With exact 16-bit products the fp32 result r
-//     lies within beta = 4 (D + 4) 2^-24 |a| |b| of the exact dot product for
-//     any summation order and rounding (norms rounded up; the constant is
-//     taken as 4.1 (D + 4) so the interval also holds the float64 sum of
-//     step 2), and rounding is monotone, so
+//     {64, 128, 256}): each of the four waves holds tok/64 tiles of 16 query
+//     vectors, split into their positive and negative parts, as MFMA A
+//     operands for the whole row. Tiles of 16 columns (their key max/min rows
+//     and norms, precomputed once per launch) stream into LDS through a
+//     3-stage ring of direct-to-LDS loads shared by the waves; the two dot
+//     products of every (vector, column) pair come from bf16/f16 MFMA with
+//     fp32 accumulation. With exact 16-bit products the fp32 result r lies
+//     within beta = 4 (D + 4) 2^-24 |a| |b| of the exact dot product for any
+//     summation order and rounding (norms rounded up; the constant is taken
+//     as 4.1 (D + 4) so the interval also holds the float64 sum of step 2),
+//     and rounding is monotone, so
 //       lo = rnd(rnd(rp - bp) + rnd(rn - bn)),  hi = rnd(rnd(rp + bp) + rnd(rn + bn))
 //     bracket the pair's score. Each column keeps max lo and max hi over its
 //     vectors. Norms outside [2^-40, 2^50] count as unbounded (bracket
 //     [-inf, inf]), which keeps the MFMA clear of overflow and of flushed
 //     subnormals.
 //  2. Exact resolution: only a column whose bracket is open and whose hi
-//     reaches the k-th largest lo can be selected without its exact score;
-//     those columns are recomputed in float64 (fixed order d = 0..D-1, one
-//     thread per (column, query vector), exact products) and the others
-//     keep hi, which is then below at least k exact scores. A row with no
-//     more columns than k needs exact values only where a bracket end is not
-//     finite (the non-finite -> own rule). fp32 operands and other block
-//     sizes skip step 1 and resolve every column.
-//  3. Top-k: a 4-pass 8-bit radix select finds the k-th largest key and how
-//     many of its ties are taken; one wave writes the taken columns in
+//     reaches the k-th largest lo can be selected without its exact score.
+//     For those columns the brackets are recomputed per query vector on the
+//     matrix cores: a closed bracket is that vector's score, and of the open
+//     ones only those whose hi reaches the column's max lo can hold the
+//     maximum; only those are recomputed in float64 (exact products, eight
+//     lanes per score with a rounding bracket that falls back to the fixed
+//     order d = 0..D-1 when it does not close). Other columns keep hi, which is then below at least k
+//     exact scores. A row with no more columns than k needs exact values
+//     only where a bracket end is not finite (the non-finite -> own rule).
+//     fp32 operands, D = 32 and other block sizes skip step 1 and compute
+//     every score in float64 (one thread per (column, query vector)).
+//  3. Top-k: an 8-bit radix select (2 passes for bf16 scores, 3 for fp16,
+//     4 for fp32) finds the k-th largest key and how many of its ties are
+//     taken; one wave writes the taken columns in
 //     ascending block order with ballots.
 #include <math.h>
 
@@ -49,14 +55,14 @@
 
 namespace fbsa {
 
-constexpr int QM_MAXCOL = 4096;  // columns per row held in LDS
-
 struct QmaxArgs {
   const void *a, *b1, *b2;
   const int32_t *cand;
   int32_t *sel;
+  float *norms;  // key-side norms: b1 rows, then b2 rows (MFMA engine)
   int64_t B, H, nblk, la, ncand;
   int tok, keff, kk, conv, sink;
+  int ncolp;  // LDS column capacity: nblk or ncand, rounded up to 8
 };
 
 // Orderable key of a score: larger scores give larger keys; -0 and +0 share
@@ -65,6 +71,9 @@ __device__ __forceinline__ uint32_t qm_key(float v) {
   if (v == 0.f) v = 0.f;
   const uint32_t u = __float_as_uint(v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float qm_key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 __device__ __forceinline__ bool qm_key_finite(uint32_t k) {
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
@@ -83,7 +92,7 @@ __device__ __forceinline__ float qm_norm(float ss, uint32_t nonzero) {
 // d = 0..D-1 (16-bit and fp32 products are exact in float64).
 template <typename T, int D> __device__ float qm_exact(const T *q, const T *k1, const T *k2) {
   double sp = 0.0, sn = 0.0;
-#pragma unroll 2
+#pragma unroll 1
   for (int d0 = 0; d0 < D; d0 += 8) {
     double v[8], x1[8], x2[8];
     load8<T>(q + d0, v);
@@ -98,26 +107,95 @@ template <typename T, int D> __device__ float qm_exact(const T *q, const T *k1, 
   return round_dt_f<T>(round_dt<T>(sp) + round_dt<T>(sn));
 }
 
-// k-th largest of keys[0, n) (1 <= k <= n) by four 8-bit radix passes; *take
-// receives how many keys equal to it are among the k largest. All 256
-// threads call it.
+// The same score with D split over the 8 lanes of a group (lane sub = 0..7
+// takes d in [sub*D/8, (sub+1)*D/8)); every lane of the group returns it. The
+// partial sums meet in another order than qm_exact's, so the result carries
+// a bracket: any summation order of the D exact products lies within
+// 2 (D - 1) 2^-53 sum|products| of the exact dot product (taken as
+// 2.1 D 2^-53 to cover this sum's own rounding), so when the rounded bracket
+// closes it equals qm_exact's value; otherwise (rare) qm_exact decides.
+template <typename T, int D> __device__ float qm_exact8(const T *q, const T *k1, const T *k2, int sub) {
+  constexpr int PER = D / 8;
+  double sp = 0.0, sn = 0.0, ap = 0.0, an = 0.0;
+#pragma unroll 1
+  for (int d0 = 0; d0 < PER; d0 += 8) {
+    double v[8], x1[8], x2[8];
+    load8<T>(q + sub * PER + d0, v);
+    load8<T>(k1 + sub * PER + d0, x1);
+    load8<T>(k2 + sub * PER + d0, x2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const double pv = v[e] > 0.0 ? v[e] : 0.0, nv = v[e] < 0.0 ? v[e] : 0.0;
+      sp = __builtin_fma(pv, x1[e], sp);
+      sn = __builtin_fma(nv, x2[e], sn);
+      ap = __builtin_fma(pv, __builtin_fabs(x1[e]), ap);
+      an = __builtin_fma(-nv, __builtin_fabs(x2[e]), an);
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) {
+    sp += __shfl_xor(sp, m, 64);
+    sn += __shfl_xor(sn, m, 64);
+    ap += __shfl_xor(ap, m, 64);
+    an += __shfl_xor(an, m, 64);
+  }
+  constexpr double C = 2.1 * D * 0x1p-53;
+  const double ep = C * ap, en = C * an;
+  const float lo = round_dt_f<T>(round_dt<T>(sp - ep) + round_dt<T>(sn - en));
+  const float hi = round_dt_f<T>(round_dt<T>(sp + ep) + round_dt<T>(sn + en));
+  if (lo == hi) return lo;
+  return qm_exact<T, D>(q, k1, k2);
+}
+
+// Sum of squares step for 16-bit pairs packed in one word: s + x0^2 + x1^2
+// (exact products; the sum's rounding is covered by the norm's 2^-10 margin).
+template <typename T> __device__ __forceinline__ float qm_dot2(uint32_t w, float s) {
+  if constexpr (__is_same(T, bf16)) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, w), __builtin_bit_cast(v2, w), s, false);
+  } else {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, w), __builtin_bit_cast(v2, w), s, false);
+  }
+}
+
+// Round an fp32 value to the operand dtype (RNE) for the brackets; no NaN
+// handling (a NaN bracket is caught by its caller), infinities stay.
+template <typename T> __device__ __forceinline__ float qm_rnd(float f) {
+  if constexpr (__is_same(T, bf16)) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xFFFF0000u);
+  } else {
+    return round_dt_f<T>(f);
+  }
+}
+
+// k-th largest of keys[0, n) (1 <= k <= n) by NP 8-bit radix passes from the
+// top; *take receives how many keys equal to it are among the k largest.
+// Keys of values on the dtype's grid vary only in their top 8*NP bits (bf16:
+// 16, fp16: 19 of 24, fp32: all 32); the rest follow from the sign. Every
+// thread of the workgroup (at least 256) calls it; hist holds 2 x 256 bins.
+template <int NP>
 __device__ uint32_t qm_radix_select(const uint32_t *keys, int n, int k, uint32_t *hist, int *sh, int *take) {
   const int tid = threadIdx.x;
   uint32_t prefix = 0, mask = 0;
   int rem = k;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
-    __syncthreads();
-    for (int c = tid; c < n; c += 256) {
+  if (tid < 256) hist[tid] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int pass = 0; pass < NP; ++pass) {
+    const int shift = 24 - 8 * pass;
+    uint32_t *h = hist + 256 * (pass & 1);
+    for (int c = tid; c < n; c += (int)blockDim.x) {
       const uint32_t key = keys[c];
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      if ((key & mask) == prefix) atomicAdd(&h[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
     if (tid < 64) {
       // lane l owns bins 4l..4l+3; find the largest bin b with
       // (keys in bins >= b) >= rem
-      const int h0 = (int)hist[4 * tid], h1 = (int)hist[4 * tid + 1], h2 = (int)hist[4 * tid + 2],
-                h3 = (int)hist[4 * tid + 3];
+      const int h0 = (int)h[4 * tid], h1 = (int)h[4 * tid + 1], h2 = (int)h[4 * tid + 2], h3 = (int)h[4 * tid + 3];
       const int tot = h0 + h1 + h2 + h3;
       int suf = tot;  // inclusive suffix sum over lanes >= l
 #pragma unroll
@@ -138,27 +216,64 @@ __device__ uint32_t qm_radix_select(const uint32_t *keys, int n, int k, uint32_t
             else { acc += h1; b = 0; }
           }
         }
-        sh[0] = 4 * tid + b;
-        sh[1] = rem - acc;
+        sh[pass & 1] = 4 * tid + b;
+        sh[2 + (pass & 1)] = rem - acc;
       }
     }
+    if (pass + 1 < NP && tid < 256) hist[256 * ((pass + 1) & 1) + tid] = 0;  // scanned two passes ago
     __syncthreads();
-    prefix |= (uint32_t)sh[0] << shift;
+    prefix |= (uint32_t)sh[pass & 1] << shift;
     mask |= 0xFFu << shift;
-    rem = sh[1];
+    rem = sh[2 + (pass & 1)];
   }
   *take = rem;
+  if constexpr (NP < 4) {
+    const uint32_t low = (1u << (32 - 8 * NP)) - 1u;
+    prefix |= (prefix & 0x80000000u) ? 0u : low;  // grid values: 0 bits below a positive key, 1 bits below a negative one
+  }
   return prefix;
 }
 
-// TOK = 64 / 128: MFMA brackets (16-bit T); TOK = 0: every column exact
-// (a.tok query vectors per block).
+template <typename T> constexpr int qm_passes() { return sizeof(T) == 4 ? 4 : __is_same(T, bf16) ? 2 : 3; }
+
+// Ring of key-block tiles for the bracket pass: 16 rows of b1 and 16 of b2
+// (16-byte chunks XOR-swizzled per row so the 16 rows x 1 chunk an MFMA B
+// operand reads fall on distinct banks) plus each wave's copy of their 32
+// norms.
+template <int D> struct QmCfg {
+  static constexpr int CPR = D / 8;
+  static constexpr int TILE_BYTES = 2 * 16 * D * 2;
+  static constexpr int NORM_BYTES = 4 * 256;  // per wave: lanes 0-15 b1, 16-31 b2 (lanes 32-63 unused)
+  static constexpr int STAGE_BYTES = TILE_BYTES + NORM_BYTES;
+  static constexpr int LPW = TILE_BYTES / 16 / 256;  // 16-byte loads per thread per tile
+  static constexpr int NSTAGE = 3;
+};
+
+// 4-byte global -> LDS copy: lane l's word lands at lds_wave_base + 4*l.
+__device__ __forceinline__ void g2lds4(const void *gsrc, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
+                                   (__attribute__((address_space(3))) void *)lds_wave_base, 4, 0, 0);
+}
+
+// Dynamic LDS: s_lo, s_hi (u32) and s_col, s_cl (u16), ncolp entries each,
+// then the tile ring (bracket pass only).
+template <int D, int TOK> static size_t qm_lds_bytes(int64_t ncolp) {
+  return (size_t)ncolp * 12 + (TOK > 0 ? (size_t)QmCfg<D>::NSTAGE * QmCfg<D>::STAGE_BYTES : 0);
+}
+
+// TOK = 64 / 128: MFMA brackets (16-bit T), each of the four waves holds
+// TOK/64 tiles of 16 query vectors; TOK = 0: every column exact (a.tok query
+// vectors per block).
 template <typename T, int D, int TOK>
-__global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
-  __shared__ uint32_t s_lo[QM_MAXCOL], s_hi[QM_MAXCOL];
-  __shared__ uint16_t s_col[QM_MAXCOL], s_cl[QM_MAXCOL];
-  __shared__ uint32_t s_hist[256];
-  __shared__ int s_sh[4];
+__global__ __launch_bounds__(256, 2) void qmax_kernel(QmaxArgs a) {
+  constexpr int NT = 256;
+  extern __shared__ __align__(16) char qm_lds[];
+  uint32_t *s_lo = (uint32_t *)qm_lds;
+  uint32_t *s_hi = s_lo + a.ncolp;
+  uint16_t *s_col = (uint16_t *)(s_hi + a.ncolp);
+  uint16_t *s_cl = s_col + a.ncolp;
+  __shared__ uint32_t s_hist[512];
+  __shared__ int s_sh[12];  // [2] candidate count, [3] contenders, [4] worklist, [8..11] radix select
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t BH = a.B * a.H;
@@ -201,40 +316,72 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
   auto col_block = [&](int c) -> int { return a.cand ? (int)s_col[c] : c; };
 
   if (keff > 0) {
-    for (int c = tid; c < count; c += 256) { s_lo[c] = 0u; s_hi[c] = 0u; }
+    for (int c = tid; c < count; c += NT) { s_lo[c] = 0u; s_hi[c] = 0u; }
     __syncthreads();
 
     // ---- 1. brackets on the matrix cores
     int nres = count;  // columns resolved exactly (TOK = 0: all of them)
     uint32_t *fin = s_lo;
     if constexpr (TOK > 0) {
+      using C = QmCfg<D>;
       constexpr int KS = D / 32, RW = TOK / 64;
       constexpr float CB = 4.1f * (float)(D + 4) * 0x1p-24f;
       const int p = lane & 15, g = lane >> 4;
+      char *ring = (char *)(s_cl + a.ncolp);
+      const float *N1 = a.norms + bh * a.nblk, *N2 = a.norms + (BH + bh) * a.nblk;
+      const int ntiles = (count + 15) / 16;
+
+      // tile tc -> ring stage tc % NSTAGE: wave-load v = l*4 + w carries
+      // chunks [64v, 64v + 64) of the tile (b1 rows, then b2 rows)
+      auto issue = [&](int tc) {
+        char *stg = ring + (tc % C::NSTAGE) * C::STAGE_BYTES;
+        const int c0 = tc * 16;
+#pragma unroll
+        for (int l = 0; l < C::LPW; ++l) {
+          const int q = (l * 4 + w) * 64 + lane;
+          const int m = q / (16 * C::CPR), r = (q / C::CPR) % 16, cp = q % C::CPR;
+          const int cc = c0 + r;
+          const int j = col_block(cc < count ? cc : count - 1);
+          g2lds16((m ? B2 : B1) + (int64_t)j * D + 8 * (cp ^ swz(r, C::CPR)), stg + (l * 4 + w) * 1024);
+        }
+        const int cc = c0 + (lane & 15);
+        const int j = col_block(cc < count ? cc : count - 1);
+        g2lds4(((lane & 16) ? N2 : N1) + j, stg + C::TILE_BYTES + w * 256);
+      };
+#pragma unroll
+      for (int tc = 0; tc < C::NSTAGE - 1; ++tc)
+        if (tc < ntiles) issue(tc);
+
+      // query vectors: split into positive and negative parts, with norms
       s16x8 ap[RW][KS], an[RW][KS];
       float cbp[RW][4], cbn[RW][4];
 #pragma unroll
       for (int x = 0; x < RW; ++x) {
+        // branch-free loads (a row past la is read clamped and zeroed), all in flight together
         const int64_t t = (int64_t)i * TOK + (w * RW + x) * 16 + p;
+        const bool tv = t < a.la;
+        const T *row = Ab + (tv ? t : a.la - 1) * D + g * 8;
+        u32x4 raw[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) raw[ks] = *(const u32x4 *)(row + ks * 32);
         float sp = 0.f, sn = 0.f;
         uint32_t zp = 0u, zn = 0u;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-          if (t < a.la) v = *(const s16x8 *)(Ab + t * D + ks * 32 + g * 8);
-          s16x8 vp, vn;
+          u32x4 vp, vn;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const bool neg = v[e] < 0;  // sign bit of the 16-bit pattern
-            vp[e] = neg ? (short)0 : v[e];
-            vn[e] = neg ? v[e] : (short)0;
-            const float f = half_bits_to_f32<T>((uint32_t)(uint16_t)v[e]);
-            const uint32_t mag = (uint32_t)(uint16_t)v[e] & 0x7FFFu;
-            if (neg) { sn = __builtin_fmaf(f, f, sn); zn |= mag; }
-            else { sp = __builtin_fmaf(f, f, sp); zp |= mag; }
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t v = tv ? raw[ks][e] : 0u;
+            const uint32_t m = ((v >> 15) & 0x00010001u) * 0xFFFFu;  // per-half sign masks
+            vn[e] = v & m;
+            vp[e] = v & ~m;
+            sp = qm_dot2<T>(vp[e], sp);
+            sn = qm_dot2<T>(vn[e], sn);
+            zp |= vp[e] & 0x7FFF7FFFu;
+            zn |= vn[e] & 0x7FFF7FFFu;
           }
-          ap[x][ks] = vp;
-          an[x][ks] = vn;
+          ap[x][ks] = __builtin_bit_cast(s16x8, vp);
+          an[x][ks] = __builtin_bit_cast(s16x8, vn);
         }
         sp += __shfl_xor(sp, 16, 64);
         sp += __shfl_xor(sp, 32, 64);
@@ -252,76 +399,52 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
           cbn[x][r] = CB * __shfl(nn, 4 * g + r, 64);
         }
       }
+      wait_vmcnt<0>();  // the query rows (and the first ring stages)
 
-      auto load_b = [&](int c0, s16x8 *bx, s16x8 *bm) {
-        const int cc = c0 + p;
-        const int j = col_block(cc < count ? cc : count - 1);
-        const T *r1 = B1 + (int64_t)j * D + g * 8;
-        const T *r2 = B2 + (int64_t)j * D + g * 8;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          bx[ks] = *(const s16x8 *)(r1 + ks * 32);
-          bm[ks] = *(const s16x8 *)(r2 + ks * 32);
-        }
-      };
-      s16x8 bx[KS], bm[KS];
-      if (count > 0) load_b(0, bx, bm);  // a candidate row may list no valid block
-      for (int c0 = 0; c0 < count; c0 += 16) {
-        // key-side norms (the 4 lanes of a column hold a quarter of each row)
-        float s1 = 0.f, s2 = 0.f;
-        uint32_t z1 = 0u, z2 = 0u;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float f1 = half_bits_to_f32<T>((uint32_t)(uint16_t)bx[ks][e]);
-            const float f2 = half_bits_to_f32<T>((uint32_t)(uint16_t)bm[ks][e]);
-            s1 = __builtin_fmaf(f1, f1, s1);
-            s2 = __builtin_fmaf(f2, f2, s2);
-            z1 |= (uint32_t)(uint16_t)bx[ks][e] & 0x7FFFu;
-            z2 |= (uint32_t)(uint16_t)bm[ks][e] & 0x7FFFu;
-          }
-        s1 += __shfl_xor(s1, 16, 64);
-        s1 += __shfl_xor(s1, 32, 64);
-        s2 += __shfl_xor(s2, 16, 64);
-        s2 += __shfl_xor(s2, 32, 64);
-        z1 |= (uint32_t)__shfl_xor((int)z1, 16, 64);
-        z1 |= (uint32_t)__shfl_xor((int)z1, 32, 64);
-        z2 |= (uint32_t)__shfl_xor((int)z2, 16, 64);
-        z2 |= (uint32_t)__shfl_xor((int)z2, 32, 64);
-        const float nb1 = qm_norm(s1, z1), nb2 = qm_norm(s2, z2);
+      for (int tc = 0; tc < ntiles; ++tc) {
+        // tile tc has landed once at most min(ahead, NSTAGE-2) later tiles are in flight
+        const int ahead = ntiles - 1 - tc;
+        wait_ring<C::LPW + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
+        // one barrier per tile: every wave has landed its part of tile tc and
+        // finished reading tile tc-1, whose stage the prefetch overwrites
+        lds_barrier();
+        if (tc + C::NSTAGE - 1 < ntiles) issue(tc + C::NSTAGE - 1);
+        const char *stg = ring + (tc % C::NSTAGE) * C::STAGE_BYTES;
+        const float nb1 = *(const float *)(stg + C::TILE_BYTES + w * 256 + 4 * p);
+        const float nb2 = *(const float *)(stg + C::TILE_BYTES + w * 256 + 64 + 4 * p);
 
         f32x4 acp[RW], acn[RW];
 #pragma unroll
         for (int x = 0; x < RW; ++x) {
           acp[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
           acn[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            acp[x] = Mfma16<T>::run(ap[x][ks], bx[ks], acp[x]);
-            acn[x] = Mfma16<T>::run(an[x][ks], bm[ks], acn[x]);
+        for (int ks = 0; ks < KS; ++ks) {
+          const int cpos = (4 * ks + g) ^ swz(p, C::CPR);
+          const s16x8 bx = *(const s16x8 *)(stg + (p * C::CPR + cpos) * 16);
+          const s16x8 bm = *(const s16x8 *)(stg + ((16 + p) * C::CPR + cpos) * 16);
+#pragma unroll
+          for (int x = 0; x < RW; ++x) {
+            acp[x] = Mfma16<T>::run(ap[x][ks], bx, acp[x]);
+            acn[x] = Mfma16<T>::run(an[x][ks], bm, acn[x]);
           }
         }
-        // the next tile's loads overlap this tile's bracket arithmetic
-        if (c0 + 16 < count) load_b(c0 + 16, bx, bm);
 
         float mlo = -INFINITY, mhi = -INFINITY;
 #pragma unroll
         for (int x = 0; x < RW; ++x)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float bp = cbp[x][r] * nb1, bn = cbn[x][r] * nb2;
-            if (bp != bp) bp = 0.f;  // 0 * inf: one side is a zero vector, its product is exact
-            if (bn != bn) bn = 0.f;
-            float lo, hi;
-            if (bp == INFINITY || bn == INFINITY) {
-              lo = -INFINITY;
-              hi = INFINITY;
-            } else {
-              const float rp = acp[x][r], rn = acn[x][r];
-              lo = round_dt_f<T>(round_dt_f<T>(rp - bp) + round_dt_f<T>(rn - bn));
-              hi = round_dt_f<T>(round_dt_f<T>(rp + bp) + round_dt_f<T>(rn + bn));
-            }
+            // 0 * inf (a zero vector against an unbounded one) is an exact 0 product: bound 0
+            const float bp = fmaxf(cbp[x][r] * nb1, 0.f), bn = fmaxf(cbn[x][r] * nb2, 0.f);
+            const float rp = acp[x][r], rn = acn[x][r];
+            float lo = qm_rnd<T>(qm_rnd<T>(rp - bp) + qm_rnd<T>(rn - bn));
+            float hi = qm_rnd<T>(qm_rnd<T>(rp + bp) + qm_rnd<T>(rn + bn));
+            // unbounded, or inf - inf after an fp16 overflow: the exact path decides
+            const bool open = bp == INFINITY || bn == INFINITY || !(lo <= hi);
+            lo = open ? -INFINITY : lo;
+            hi = open ? INFINITY : hi;
             mlo = fmaxf(mlo, lo);
             mhi = fmaxf(mhi, hi);
           }
@@ -329,7 +452,7 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
         mlo = fmaxf(mlo, __shfl_xor(mlo, 32, 64));
         mhi = fmaxf(mhi, __shfl_xor(mhi, 16, 64));
         mhi = fmaxf(mhi, __shfl_xor(mhi, 32, 64));
-        const int cc = c0 + p;
+        const int cc = tc * 16 + p;
         if (g == 0 && cc < count) {
           atomicMax(&s_lo[cc], qm_key(mlo));
           atomicMax(&s_hi[cc], qm_key(mhi));
@@ -341,39 +464,94 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
       uint32_t tau = 0u;
       if (count > keff) {
         int dummy;
-        tau = qm_radix_select(s_lo, count, keff, s_hist, s_sh, &dummy);
+        tau = qm_radix_select<qm_passes<T>()>(s_lo, count, keff, s_hist, s_sh + 8, &dummy);
       }
       if (tid == 0) s_sh[3] = 0;
       __syncthreads();
-      for (int c = tid; c < count; c += 256) {
+      for (int c = tid; c < count; c += NT) {
         const uint32_t lo = s_lo[c], hi = s_hi[c];
         const bool need = count > keff ? (lo != hi && hi >= tau) : !(qm_key_finite(lo) && qm_key_finite(hi));
         if (need) {
           const int n = atomicAdd(&s_sh[3], 1);
           s_cl[n] = (uint16_t)c;
-          s_lo[c] = 0u;
+          s_hi[c] = 0u;  // rebuilt below as the exact column maximum
         }
       }
       __syncthreads();
       nres = s_sh[3];
       fin = s_hi;
-    }
 
-    // ---- 2. exact scores (one thread per (column, query vector))
-    const int64_t items = (int64_t)nres * tok;
-    for (int64_t it = tid; it < items; it += 256) {
-      const int n = (int)(it / tok), t = (int)(it % tok);
-      const int c = TOK > 0 ? (int)s_cl[n] : n;
-      const int j = col_block(c);
-      const int64_t tr = (int64_t)i * tok + t;
-      const float v = tr < a.la ? qm_exact<T, D>(Ab + tr * D, B1 + (int64_t)j * D, B2 + (int64_t)j * D) : 0.f;
-      atomicMax(&s_lo[c], qm_key(v));
-    }
-    __syncthreads();
-    if constexpr (TOK > 0) {
-      for (int n = tid; n < nres; n += 256) {
-        const int c = s_cl[n];
-        s_hi[c] = s_lo[c];
+      // ---- 2. exact maxima of the contenders, 16 at a time: the brackets are
+      // recomputed per query vector on the matrix cores; a closed bracket is
+      // the vector's score, and of the open ones only those whose hi reaches
+      // the column's max lo can hold the maximum (the vector behind max lo
+      // among them), so only those go to float64 (a worklist in the free ring)
+      uint32_t *work = (uint32_t *)ring;  // (slot << 8 | vector), at most 16 * TOK per tile
+      for (int t0 = 0; t0 < nres; t0 += 16) {
+        if (tid == 0) s_sh[4] = 0;
+        const bool live = t0 + p < nres;
+        const int c = s_cl[live ? t0 + p : nres - 1];
+        const int j = col_block(c);
+        const T *r1 = B1 + (int64_t)j * D + g * 8, *r2 = B2 + (int64_t)j * D + g * 8;
+        const float nb1 = N1[j], nb2 = N2[j];
+        const float mlo_c = qm_key_value(s_lo[c]);
+        f32x4 acp[RW], acn[RW];
+#pragma unroll
+        for (int x = 0; x < RW; ++x) {
+          acp[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
+          acn[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const s16x8 bx = *(const s16x8 *)(r1 + ks * 32), bm = *(const s16x8 *)(r2 + ks * 32);
+#pragma unroll
+          for (int x = 0; x < RW; ++x) {
+            acp[x] = Mfma16<T>::run(ap[x][ks], bx, acp[x]);
+            acn[x] = Mfma16<T>::run(an[x][ks], bm, acn[x]);
+          }
+        }
+        __syncthreads();  // s_sh[4] cleared; the previous worklist is consumed
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < RW; ++x)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float bp = fmaxf(cbp[x][r] * nb1, 0.f), bn = fmaxf(cbn[x][r] * nb2, 0.f);
+            const float rp = acp[x][r], rn = acn[x][r];
+            const float lo = qm_rnd<T>(qm_rnd<T>(rp - bp) + qm_rnd<T>(rn - bn));
+            const float hi = qm_rnd<T>(qm_rnd<T>(rp + bp) + qm_rnd<T>(rn + bn));
+            const bool open = bp == INFINITY || bn == INFINITY || !(lo == hi);
+            if (!open) cmax = fmaxf(cmax, lo);
+            else if (live && !(hi < mlo_c)) {
+              const int slot = atomicAdd(&s_sh[4], 1);
+              work[slot] = ((uint32_t)p << 8) | (uint32_t)((w * RW + x) * 16 + 4 * g + r);
+            }
+          }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        if (g == 0 && live) atomicMax(&s_hi[c], qm_key(cmax));
+        __syncthreads();
+        const int nw = s_sh[4];
+        for (int it = tid >> 3; it < nw; it += NT / 8) {  // 8 lanes per item
+          const uint32_t e = work[it];
+          const int c2 = s_cl[t0 + (int)(e >> 8)];
+          const int j2 = col_block(c2);
+          const int64_t tr = (int64_t)i * TOK + (e & 255u);
+          const float v = tr < a.la ? qm_exact8<T, D>(Ab + tr * D, B1 + (int64_t)j2 * D, B2 + (int64_t)j2 * D, tid & 7)
+                                    : 0.f;
+          if ((tid & 7) == 0) atomicMax(&s_hi[c2], qm_key(v));
+        }
+        __syncthreads();
+      }
+    } else {
+      // ---- 2. exact scores of every column (one thread per (column, query vector))
+      const int64_t items = (int64_t)nres * tok;
+      for (int64_t it = tid; it < items; it += NT) {
+        const int c = (int)(it / tok), t = (int)(it % tok);
+        const int j = col_block(c);
+        const int64_t tr = (int64_t)i * tok + t;
+        const float v = tr < a.la ? qm_exact<T, D>(Ab + tr * D, B1 + (int64_t)j * D, B2 + (int64_t)j * D) : 0.f;
+        atomicMax(&s_lo[c], qm_key(v));
       }
       __syncthreads();
     }
@@ -382,7 +560,7 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
     const bool all = count <= keff;
     uint32_t tau2 = 0u;
     int take_eq = 0;
-    if (!all) tau2 = qm_radix_select(fin, count, keff, s_hist, s_sh, &take_eq);
+    if (!all) tau2 = qm_radix_select<qm_passes<T>()>(fin, count, keff, s_hist, s_sh + 8, &take_eq);
     if (w == 0) {
       int nfin = 0, eqseen = 0;
       for (int c0 = 0; c0 < count; c0 += 64) {
@@ -411,37 +589,86 @@ __global__ __launch_bounds__(256) void qmax_kernel(QmaxArgs a) {
   }
 }
 
-template <typename T, int D> static void launch_qmax_d(const QmaxArgs &a, bool exact, hipStream_t s) {
-  const dim3 grid((unsigned)(a.B * a.H * a.nblk)), block(256);
-  if constexpr (sizeof(T) == 2) {
-    if (!exact && a.tok == 64) { hipLaunchKernelGGL((qmax_kernel<T, D, 64>), grid, block, 0, s, a); return; }
-    if (!exact && a.tok == 128) { hipLaunchKernelGGL((qmax_kernel<T, D, 128>), grid, block, 0, s, a); return; }
+// Key-side norms for the MFMA engine: one thread per key block row of b1 and
+// of b2, the same rounded-up bound the query side uses.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void qm_norms_kernel(QmaxArgs a) {
+  const int64_t n = a.B * a.H * a.nblk;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= 2 * n) return;
+  const T *row = (const T *)(r < n ? a.b1 : a.b2) + (r < n ? r : r - n) * D;
+  float ss = 0.f;
+  uint32_t z = 0u;
+#pragma unroll 4
+  for (int d0 = 0; d0 < D; d0 += 8) {
+    const u32x4 w = *(const u32x4 *)(row + d0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ss = qm_dot2<T>(w[e], ss);
+      z |= w[e] & 0x7FFF7FFFu;
+    }
   }
-  hipLaunchKernelGGL((qmax_kernel<T, D, 0>), grid, block, 0, s, a);
+  a.norms[r] = qm_norm(ss, z);
+}
+
+template <typename T, int D, int TOK> static int launch_qmax_k(const QmaxArgs &a, hipStream_t s) {
+  const size_t lds = qm_lds_bytes<D, TOK>(a.ncolp);
+  if (lds > 64 * 1024) {
+    static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation
+    if (lds > attr_bytes) {
+      int e = hip_check(hipFuncSetAttribute((const void *)qmax_kernel<T, D, TOK>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                        "hipFuncSetAttribute(qmax)");
+      if (e) return e;
+      attr_bytes = lds;
+    }
+  }
+  hipLaunchKernelGGL((qmax_kernel<T, D, TOK>), dim3((unsigned)(a.B * a.H * a.nblk)), dim3(256), lds, s, a);
+  return FBSA_OK;
+}
+
+template <typename T, int D> static int launch_qmax_d(const QmaxArgs &a, bool exact, hipStream_t s) {
+  if constexpr (sizeof(T) == 2 && D >= 64) {
+    if (!exact && (a.tok == 64 || a.tok == 128)) {
+      const int64_t nrow = 2 * a.B * a.H * a.nblk;
+      hipLaunchKernelGGL((qm_norms_kernel<T, D>), dim3((unsigned)((nrow + 255) / 256)), dim3(256), 0, s, a);
+      return a.tok == 64 ? launch_qmax_k<T, D, 64>(a, s) : launch_qmax_k<T, D, 128>(a, s);
+    }
+  }
+  return launch_qmax_k<T, D, 0>(a, s);
 }
 
 template <typename T> static int launch_qmax(const QmaxArgs &a, int64_t D, bool exact, hipStream_t s) {
+  int e = FBSA_OK;
   switch (D) {
-    case 32: launch_qmax_d<T, 32>(a, exact, s); break;
-    case 64: launch_qmax_d<T, 64>(a, exact, s); break;
-    case 128: launch_qmax_d<T, 128>(a, exact, s); break;
-    case 256: launch_qmax_d<T, 256>(a, exact, s); break;
+    case 32: e = launch_qmax_d<T, 32>(a, exact, s); break;
+    case 64: e = launch_qmax_d<T, 64>(a, exact, s); break;
+    case 128: e = launch_qmax_d<T, 128>(a, exact, s); break;
+    case 256: e = launch_qmax_d<T, 256>(a, exact, s); break;
     default: return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: operand dim %lld not in {32,64,128,256}", (long long)D);
   }
+  if (e) return e;
   return hip_check(hipGetLastError(), "qmax_kernel launch");
 }
 
+size_t select_qmax_workspace_bytes(const fbsa_qmax_desc *d) {
+  const bool mfma = d->dtype != FBSA_F32 && (d->tok == 64 || d->tok == 128) && d->D >= 64 &&
+                    !(d->flags & FBSA_QMAX_EXACT);
+  return mfma ? (size_t)(2 * d->B * d->H * d->nblk) * sizeof(float) : 0;
+}
+
 int run_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2, const int32_t *cand,
-                    int32_t *sel, hipStream_t s) {
+                    int32_t *sel, void *ws, hipStream_t s) {
   QmaxArgs q;
-  q.a = a; q.b1 = b1; q.b2 = b2; q.cand = cand; q.sel = sel;
+  q.a = a; q.b1 = b1; q.b2 = b2; q.cand = cand; q.sel = sel; q.norms = (float *)ws;
   q.B = d->B; q.H = d->H; q.nblk = d->nblk; q.la = d->la; q.ncand = cand ? d->ncand : 0;
+  q.ncolp = (int)(((cand ? d->ncand : d->nblk) + 7) & ~7LL);
   q.tok = (int)d->tok;
   q.keff = (int)(d->topk < d->nblk ? d->topk : d->nblk);
   q.kk = (int)d->kk;
   q.conv = d->convention;
   q.sink = d->sink;
-  const bool exact = (d->flags & FBSA_QMAX_EXACT) != 0;
+  const bool exact = (d->flags & FBSA_QMAX_EXACT) != 0 || ws == nullptr;
   switch (d->dtype) {
     case FBSA_BF16: return launch_qmax<bf16>(q, d->D, exact, s);
     case FBSA_F16: return launch_qmax<f16>(q, d->D, exact, s);

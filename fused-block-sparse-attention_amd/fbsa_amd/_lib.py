@@ -85,7 +85,9 @@ SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "fbsa_select_rows": (ctypes.c_int, [ctypes.POINTER(SelectDesc), ctypes.c_int64, ctypes.c_int64,
                                         _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
-    "fbsa_select_qmax": (ctypes.c_int, [ctypes.POINTER(QmaxDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fbsa_select_qmax_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(QmaxDesc)]),
+    "fbsa_select_qmax": (ctypes.c_int, [ctypes.POINTER(QmaxDesc), _vp, _vp, _vp, _vp, _vp, _vp,
+                                        ctypes.c_size_t, _vp]),
     "fbsa_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnDesc)]),
     "fbsa_bwd_prep": (ctypes.c_int, [ctypes.POINTER(AttnDesc)] + [_vp] * 6 + [ctypes.c_size_t, _vp]),
     "fbsa_transpose_index": (ctypes.c_int, [ctypes.POINTER(AttnDesc), _vp, _vp, ctypes.c_size_t, _vp]),

@@ -238,8 +238,11 @@ def select_qmax(a, b1, b2, tok, *, topk, convention="sorted_sink", sink=True, ca
         cand = cand.contiguous()
         d.ncand = cand.shape[3]
     sel = torch.empty(B, H, nblk, kk, dtype=torch.int32, device=a.device)
-    _lib.check(_lib.load().fbsa_select_qmax(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(cand), _ptr(sel), _stream()),
-               "fbsa_select_qmax")
+    lib = _lib.load()
+    nbytes = lib.fbsa_select_qmax_workspace_bytes(d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    _lib.check(lib.fbsa_select_qmax(d, _ptr(a), _ptr(b1), _ptr(b2), _ptr(cand), _ptr(sel), _ptr(ws), nbytes,
+                                    _stream()), "fbsa_select_qmax")
     return sel
 
 

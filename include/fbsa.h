@@ -183,10 +183,11 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
  * a: (B,H,la,D) contiguous query vectors, block i = vectors [i*tok,
  * (i+1)*tok), vectors at or past la are zero (the reference's zero padding);
  * b1, b2: (B,H,nblk,D) contiguous; sel: (B,H,nblk,kk). Operands are finite.
- * 16-bit operands with tok 64 or 128 bracket the scores on MFMA and compute
- * exactly (float64) only the scores the top-k needs; other cases, or
- * FBSA_QMAX_EXACT, compute every score in float64; both give the same
- * result. Supports D in {32,64,128,256}, nblk <= 65536 and at most 4096
+ * 16-bit operands with tok 64 or 128, D >= 64 and a workspace of at least
+ * fbsa_select_qmax_workspace_bytes() bytes (16-byte aligned; it holds the
+ * key-block norms) bracket the scores on MFMA and compute exactly (float64)
+ * only the scores the top-k needs; other cases, no workspace, or
+ * FBSA_QMAX_EXACT compute every score in float64; all give the same result. Supports D in {32,64,128,256}, nblk <= 65536 and at most 4096
  * columns per row (nblk, or ncand with a candidate list). Replaces
  * SelectMaxQMax.select (tok = bs, a = the GQA-group mean of every token;
  * src/qwen_blocksparse.py:216-241) and both stages of SelectTwoStage
@@ -199,8 +200,10 @@ typedef struct fbsa_qmax_desc {
   int64_t B, H, nblk, D, tok, la, topk, kk, ncand;
 } fbsa_qmax_desc;
 
+size_t fbsa_select_qmax_workspace_bytes(const fbsa_qmax_desc *d);
 int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, const void *b2,
-                     const int32_t *cand, int32_t *sel, void *stream);
+                     const int32_t *cand, int32_t *sel, void *workspace, size_t workspace_bytes,
+                     void *stream);
 
 /* ---- backward -------------------------------------------------------- */
 
