@@ -42,7 +42,8 @@
 //     exact scores. A row with no more columns than k needs exact values
 //     only where a bracket end is not finite (the non-finite -> own rule).
 //     fp32 operands, D = 32 and other block sizes skip step 1 and compute
-//     every score in float64 (one thread per (column, query vector)).
+//     every score in float64 (eight lanes per (column, query vector) with the
+//     same rounding bracket from D = 64 on).
 //  3. Top-k: an 8-bit radix select (2 passes for bf16 scores, 3 for fp16,
 //     4 for fp32) finds the k-th largest key and how many of its ties are
 //     taken; one wave writes the taken columns in
@@ -114,10 +115,12 @@ template <typename T, int D> __device__ float qm_exact(const T *q, const T *k1, 
 // 2 (D - 1) 2^-53 sum|products| of the exact dot product (taken as
 // 2.1 D 2^-53 to cover this sum's own rounding), so when the rounded bracket
 // closes it equals qm_exact's value; otherwise (rare) qm_exact decides.
-template <typename T, int D> __device__ float qm_exact8(const T *q, const T *k1, const T *k2, int sub) {
-  constexpr int PER = D / 8;
+// FULL unrolls the loads (all in flight at once) where registers allow.
+template <typename T, int D, bool FULL = false>
+__device__ float qm_exact8(const T *q, const T *k1, const T *k2, int sub) {
+  constexpr int PER = D / 8, UNROLL = FULL ? PER / 8 : 1;
   double sp = 0.0, sn = 0.0, ap = 0.0, an = 0.0;
-#pragma unroll 1
+#pragma unroll UNROLL
   for (int d0 = 0; d0 < PER; d0 += 8) {
     double v[8], x1[8], x2[8];
     load8<T>(q + sub * PER + d0, v);
@@ -168,6 +171,31 @@ template <typename T> __device__ __forceinline__ float qm_rnd(float f) {
     return __uint_as_float(u & 0xFFFF0000u);
   } else {
     return round_dt_f<T>(f);
+  }
+}
+
+// Bracket of one (vector, column) score from the fp32 MFMA sums rp, rn and
+// their error bounds bp, bn: lo = rnd(rnd(rp - bp) + rnd(rn - bn)), hi =
+// rnd(rnd(rp + bp) + rnd(rn + bn)). For bf16 the six roundings go through the
+// packed hardware conversion (v_cvt_pk_bf16_f32: round to nearest even, equal
+// to the integer rounding above for every non-NaN fp32 input).
+template <typename T> __device__ __forceinline__ void qm_bracket(float rp, float rn, float bp, float bn, float &lo,
+                                                                 float &hi) {
+  if constexpr (__is_same(T, bf16)) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    auto rnd2 = [](float x, float y, float &rx, float &ry) {
+      const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){x, y}, v2));
+      rx = __uint_as_float(u << 16);
+      ry = __uint_as_float(u & 0xFFFF0000u);
+    };
+    float lp, ln, hp, hn;
+    rnd2(rp - bp, rn - bn, lp, ln);
+    rnd2(rp + bp, rn + bn, hp, hn);
+    rnd2(lp + ln, hp + hn, lo, hi);
+  } else {
+    lo = qm_rnd<T>(qm_rnd<T>(rp - bp) + qm_rnd<T>(rn - bn));
+    hi = qm_rnd<T>(qm_rnd<T>(rp + bp) + qm_rnd<T>(rn + bn));
   }
 }
 
@@ -438,9 +466,8 @@ __global__ __launch_bounds__(256, 2) void qmax_kernel(QmaxArgs a) {
           for (int r = 0; r < 4; ++r) {
             // 0 * inf (a zero vector against an unbounded one) is an exact 0 product: bound 0
             const float bp = fmaxf(cbp[x][r] * nb1, 0.f), bn = fmaxf(cbn[x][r] * nb2, 0.f);
-            const float rp = acp[x][r], rn = acn[x][r];
-            float lo = qm_rnd<T>(qm_rnd<T>(rp - bp) + qm_rnd<T>(rn - bn));
-            float hi = qm_rnd<T>(qm_rnd<T>(rp + bp) + qm_rnd<T>(rn + bn));
+            float lo, hi;
+            qm_bracket<T>(acp[x][r], acn[x][r], bp, bn, lo, hi);
             // unbounded, or inf - inf after an fp16 overflow: the exact path decides
             const bool open = bp == INFINITY || bn == INFINITY || !(lo <= hi);
             lo = open ? -INFINITY : lo;
@@ -517,9 +544,8 @@ __global__ __launch_bounds__(256, 2) void qmax_kernel(QmaxArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float bp = fmaxf(cbp[x][r] * nb1, 0.f), bn = fmaxf(cbn[x][r] * nb2, 0.f);
-            const float rp = acp[x][r], rn = acn[x][r];
-            const float lo = qm_rnd<T>(qm_rnd<T>(rp - bp) + qm_rnd<T>(rn - bn));
-            const float hi = qm_rnd<T>(qm_rnd<T>(rp + bp) + qm_rnd<T>(rn + bn));
+            float lo, hi;
+            qm_bracket<T>(acp[x][r], acn[x][r], bp, bn, lo, hi);
             const bool open = bp == INFINITY || bn == INFINITY || !(lo == hi);
             if (!open) cmax = fmaxf(cmax, lo);
             else if (live && !(hi < mlo_c)) {
@@ -544,14 +570,22 @@ __global__ __launch_bounds__(256, 2) void qmax_kernel(QmaxArgs a) {
         __syncthreads();
       }
     } else {
-      // ---- 2. exact scores of every column (one thread per (column, query vector))
+      // ---- 2. exact scores of every column (eight lanes per (column, query
+      // vector) from D = 64 on, one thread below)
       const int64_t items = (int64_t)nres * tok;
-      for (int64_t it = tid; it < items; it += NT) {
+      constexpr int LPI = D >= 64 ? 8 : 1;
+      for (int64_t it = tid / LPI; it < items; it += NT / LPI) {
         const int c = (int)(it / tok), t = (int)(it % tok);
         const int j = col_block(c);
         const int64_t tr = (int64_t)i * tok + t;
-        const float v = tr < a.la ? qm_exact<T, D>(Ab + tr * D, B1 + (int64_t)j * D, B2 + (int64_t)j * D) : 0.f;
-        atomicMax(&s_lo[c], qm_key(v));
+        float v = 0.f;
+        if (tr < a.la) {
+          if constexpr (D >= 64)
+            v = qm_exact8<T, D, true>(Ab + tr * D, B1 + (int64_t)j * D, B2 + (int64_t)j * D, tid & 7);
+          else
+            v = qm_exact<T, D>(Ab + tr * D, B1 + (int64_t)j * D, B2 + (int64_t)j * D);
+        }
+        if (tid % LPI == 0) atomicMax(&s_lo[c], qm_key(v));
       }
       __syncthreads();
     }

@@ -25,6 +25,13 @@
 namespace fbsa {
 
 // ---------------------------------------------------------------- pooling
+// x / n for a mean: a multiplication when n is a power of two (the reciprocal
+// is exact, so the quotient is identical), an IEEE division otherwise.
+__device__ __forceinline__ double mean_div(double x, int64_t n) {
+  if ((n & (n - 1)) == 0) return x * (1.0 / (double)n);
+  return x / (double)n;
+}
+
 struct PoolArgs {
   const void *x;
   void *out, *out2;
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
         for (int e = 0; e < 8; ++e) {
           double tot = 0.0;
           for (int l = 0; l < TL; ++l) tot += red[(l * DC + tid) * 8 + e];
-          hsum[e] += (double)round_dt<T>(tot / (double)a.bs);
+          hsum[e] += (double)round_dt<T>(mean_div(tot, a.bs));
         }
       }
       __syncthreads();
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
     if (tid < DC) {
       T *o = (T *)a.out + ((b * a.Ho + ho) * a.nblk + i) * a.D + 8 * tid;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (T)round_dt<T>(hsum[e] / (double)a.grp);
+      for (int e = 0; e < 8; ++e) o[e] = (T)round_dt<T>(mean_div(hsum[e], a.grp));
     }
     return;
   }
@@ -136,7 +143,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
             for (int e = 0; e < 8; ++e) g[e] += v[e];
           }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += (double)round_dt<T>(g[e] / (double)a.grp);
+        for (int e = 0; e < 8; ++e) acc[e] += (double)round_dt<T>(mean_div(g[e], a.grp));
       }
   } else {
     // MAX / MIN / MINMAX over tokens (padding tokens count as 0)
@@ -187,7 +194,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
     T *o = (T *)a.out + off;
     if (op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (T)round_dt<T>(res[e] / (double)a.bs);
+      for (int e = 0; e < 8; ++e) o[e] = (T)round_dt<T>(mean_div(res[e], a.bs));
     } else if (op == FBSA_POOL_MAX) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (T)(float)res2[e];
@@ -277,7 +284,7 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
       }
       const bool ok = t < nval && t < BS;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r0[e] += ok ? (double)round_dt<T>(g[e] / (double)a.grp) : 0.0;
+      for (int e = 0; e < 8; ++e) r0[e] += ok ? (double)round_dt<T>(mean_div(g[e], a.grp)) : 0.0;
     }
     xor_sum(r0);
   } else {
@@ -324,8 +331,7 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
       double tot = 0.0;
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww) tot += red[0][ww][cc][e];
-      const double den = op == FBSA_POOL_MEAN_TOK_THEN_GRP ? (double)a.grp : (double)BS;
-      ((T *)a.out)[off] = (T)round_dt<T>(tot / den);
+      ((T *)a.out)[off] = (T)round_dt<T>(mean_div(tot, op == FBSA_POOL_MEAN_TOK_THEN_GRP ? a.grp : (int64_t)BS));
     } else {
       double mn = red[0][0][cc][e], mx = red[1][0][cc][e];
 #pragma unroll
@@ -353,16 +359,26 @@ __global__ __launch_bounds__(256) void pool_grp_kernel(PoolArgs a, int64_t n) {
   double s[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) s[e] = 0.0;
+  const T *base = (const T *)a.x + b * a.sx[0] + ho * a.grp * a.sx[1] + t * a.sx[2] + 8 * c;
   if (t < a.l_valid)
-    for (int64_t hh = 0; hh < a.grp; ++hh) {
-      double v[8];
-      load8<T>((const T *)a.x + b * a.sx[0] + (ho * a.grp + hh) * a.sx[1] + t * a.sx[2] + 8 * c, v);
+    for (int64_t h0 = 0; h0 < a.grp; h0 += 8) {
+      // up to eight heads' loads in flight before any is summed
+      Raw8<T> raw[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s[e] += v[e];
+      for (int u = 0; u < 8; ++u)
+        if (h0 + u < a.grp) raw[u] = load_raw8<T>(base + (h0 + u) * a.sx[1]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (h0 + u < a.grp) {
+          double v[8];
+          decode8<T>(raw[u], v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[e] += v[e];
+        }
     }
   T r[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (T)round_dt<T>(s[e] / (double)a.grp);
+  for (int e = 0; e < 8; ++e) r[e] = (T)round_dt<T>(mean_div(s[e], a.grp));
   T *o = (T *)a.out + ((b * a.Ho + ho) * a.nblk + t) * a.D + 8 * c;
   if (((uintptr_t)o & 15) == 0) {
     uint4 u[sizeof(T) / 2];
