@@ -10,7 +10,10 @@ state-dict names and training hooks (``src/ssa_model.py:93-201``):
   sq . sk_max) (``:113-119``), still available for callers that want the
   dense matrix (``src/bench_crossover.py:43``);
 * ``last_block_logits`` (the last query block's raw row), ``last_hit`` (with
-  ``needle_pos``), ``distill`` / ``distill_logits`` / ``distill_target``.
+  ``needle_pos``), ``distill`` / ``distill_logits`` / ``distill_target``
+  (``:138-149``; for 16-bit models with block 64/128 and head dim 64/128/256
+  the dense per-block mass comes from the fused block-mass kernel instead of an
+  (B, H, L, L) probability matrix).
 
 The forward never forms the nblk x nblk score matrix: the block-pooled
 selector features go to the streaming top-k kernel (own block first, then
@@ -114,10 +117,19 @@ class BlockSparseSSA(nn.Module):
 
         if self.distill:
             scale = dh ** -0.5
-            att = (q @ k.transpose(-1, -2)) * scale
-            future_tok = torch.triu(torch.ones(Lp, Lp, dtype=torch.bool, device=dev), 1)
-            att = att.masked_fill(future_tok, float("-inf")).softmax(-1)
-            mass = att.view(B, H, nblk, Bs, nblk, Bs).sum(-1).mean(3)
+            if q.dtype in (torch.bfloat16, torch.float16) and Bs in (64, 128) and dh in (64, 128, 256):
+                # the dense causal per-block mass on the fused kernel: no (B, H, Lp, Lp)
+                # matrix; scores rounded as the 16-bit matmul and scale multiply round
+                # them, fp32 softmax (the autocast case; without autocast torch's
+                # softmax output is additionally rounded to q's dtype)
+                mass = ops.block_mass(q.detach(), k.detach(), Bs, scale)
+                if not torch.is_autocast_enabled():
+                    mass = mass.to(q.dtype)
+            else:
+                att = (q @ k.transpose(-1, -2)) * scale
+                future_tok = torch.triu(torch.ones(Lp, Lp, dtype=torch.bool, device=dev), 1)
+                att = att.masked_fill(future_tok, float("-inf")).softmax(-1)
+                mass = att.view(B, H, nblk, Bs, nblk, Bs).sum(-1).mean(3)
             self.distill_target = mass.mean(1).detach()
             ar = torch.arange(nblk, device=dev)
             raw = torch.maximum(sq @ sk_mean.transpose(-1, -2), sq @ sk_max.transpose(-1, -2))

@@ -125,6 +125,34 @@ def test_blocksparse_module_matches_oracle(causal, gate):
     assert_close(np64(a), ref, "bf16", "module out")
 
 
+@pytest.mark.parametrize("dtype,L,autocast", [("bf16", 1024, False), ("bf16", 1000, True), ("f32", 512, False)])
+def test_blocksparse_distill_target_matches_oracle(dtype, L, autocast):
+    # self-distillation target (src/ssa_model.py:140-149): dense causal softmax of
+    # the module's own q, k summed per key block, averaged over each query
+    # block's rows and the heads; 16-bit models take the fused block-mass kernel
+    from ssa_model import BlockSparseSSA
+    torch.manual_seed(4)
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    m = BlockSparseSSA(256, 4, block=64, topk=3, causal=True).to(DEV).to(tdt)
+    m.distill = True
+    x = torch.randn(1, L, 256, device=DEV, dtype=tdt)
+    _say("distill", dtype, L, autocast)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        m(x)
+        Lp = (L + 63) // 64 * 64
+        xp = F.pad(x, (0, 0, 0, Lp - L))
+        q, k, _ = (t.view(1, Lp, 4, 64).transpose(1, 2) for t in m.qkv(xp).chunk(3, -1))
+    tgt = m.distill_target
+    assert tgt.shape == (1, Lp // 64, Lp // 64)
+    assert tgt.dtype == (torch.float32 if autocast or dtype == "f32" else tdt)
+    ref = oattn.block_mass(np64(q), np64(k), 64, 64 ** -0.5, "f32" if q.dtype == torch.float32 else "bf16")
+    ref = ref.mean(1)
+    atol = 5e-5 if tgt.dtype == torch.float32 else 4e-3  # a bf16 target carries its own rounding
+    np.testing.assert_allclose(np64(tgt), ref, atol=atol, rtol=0)
+    np.testing.assert_allclose(np64(tgt).sum(-1), 1.0, atol=atol * 64)
+    assert m.distill_logits.shape == tgt.shape
+
+
 def test_blocksparse_gate_gradient_paths():
     # gather path (use_triton=False) trains the selector through the gate; the
     # fused op (use_triton=True) returns no gate gradient (src/triton_kernel.py:254)
