@@ -16,6 +16,8 @@ Restates, in numpy, the reference's block-pair selection:
 * ``select_conv_a`` -- own block first + top-k content blocks
   (``src/ssa_model.py:151-165``; ``src/bench_crossover.py:41-54``).
 * ``select_conv_b`` -- ``_finish`` (``src/qwen_blocksparse.py:87-99``).
+* ``bucket_members`` / ``centroid_route`` / ``lsh_route`` / ``lsh_dense`` -- the
+  routing of ``CentroidSSA`` and ``LSHBucketSSA`` (``src/ssa_model.py:204-513``).
 * ``pool_grp_mean_tok`` / ``scores_qmax`` / ``select_topk_set`` -- the
   token-max Quest score of ``SelectMaxQMax`` and the two stages of
   ``SelectTwoStage`` (``src/qwen_blocksparse.py:216-241``, ``:267-299``).
@@ -328,6 +330,109 @@ def select_two_stage(q, k, bs, topk, sink, over, dtype):
     cand = select_topk_set(s1, min(over * topk, nblk))
     s2 = scores_qmax(qg, kmax, kmin, bs, dtype, cand=cand)
     return select_conv_b(s2, topk, sink), s2, cand
+
+
+def bucket_members(home, n_buckets, cap):
+    """(B, n) bucket id per block -> (B, n_buckets, cap) ids of each bucket's
+    first cap members in block order, -1 for unused places (the fixed-capacity
+    buckets of ``src/ssa_model.py:269-275``, ``:430-436``), by a plain loop."""
+    home = np.asarray(home)
+    B, n = home.shape
+    out = np.full((B, n_buckets, cap), -1, dtype=np.int64)
+    for b in range(B):
+        fill = np.zeros(n_buckets, dtype=np.int64)
+        for j in range(n):
+            c = home[b, j]
+            if fill[c] < cap:
+                out[b, c, fill[c]] = j
+                fill[c] += 1
+    return out
+
+
+def centroid_route(sq, sk, cent, cpq, cap, refine_topk=None, qm=None, km=None):
+    """``CentroidSSA`` routing (``src/ssa_model.py:256-301``) on float64 values:
+    qc = sq.cent^T, kc = sk.cent^T, each key block's centroid argmax(kc), each
+    query block's top-cpq centroids, their buckets' members (own block
+    removed), optional re-rank of the candidates by qm.km (block means of the
+    main q, k) to refine_topk. Returns (slots (B,nblk,kk) int64 with -1 for
+    empty places, qc, kc, home)."""
+    sq, sk, cent = (np.asarray(a, dtype=np.float64) for a in (sq, sk, cent))
+    B, nblk, _ = sq.shape
+    C = cent.shape[0]
+    cpq, cap = min(cpq, C), min(cap, nblk)
+    qc, kc = sq @ cent.T, sk @ cent.T
+    home = kc.argmax(-1)
+    routes = np.argsort(-qc, axis=-1, kind="stable")[..., :cpq]
+    members = bucket_members(home, C, cap)
+    slots = np.stack([np.concatenate([members[b, routes[b, i]].ravel() for i in range(nblk)]).reshape(nblk, -1)
+                      for b in range(B)])
+    own = np.arange(nblk)[None, :, None]
+    slots = np.where(slots == own, -1, slots)
+    if refine_topk is not None and refine_topk < cpq * cap:
+        qm, km = np.asarray(qm, dtype=np.float64), np.asarray(km, dtype=np.float64)
+        sc = np.einsum("bid,bipd->bip", qm, km[np.arange(B)[:, None, None], np.maximum(slots, 0)])
+        sc = np.where(slots >= 0, sc, -np.inf)
+        order = np.argsort(-sc, axis=-1, kind="stable")[..., :min(refine_topk, cpq * cap)]
+        slots = np.take_along_axis(slots, order, -1)
+    slots = np.concatenate([np.broadcast_to(own, (B, nblk, 1)), slots], -1)
+    return slots, qc, kc, home
+
+
+def lsh_route(sq, sk, R, cap, scale, causal, topk):
+    """``LSHBucketSSA`` bucketed selection (``src/ssa_model.py:425-452``): per
+    round, hash = argmax of the projection on R[:, r, :]; candidates = the
+    first cap members of the query block's bucket, concatenated over rounds;
+    a place is dropped if empty, a repeat of an earlier place (compared on
+    ids with empty places read as block 0, as the reference compares them),
+    the own block or (causal) a future block; the rest are scored
+    scale * sq.sk and the top min(k, places) kept. Returns (slots (B,nblk,kk)
+    with -1 for invalid picks, own first; their scores, own score first)."""
+    sq, sk, R = (np.asarray(a, dtype=np.float64) for a in (sq, sk, R))
+    B, nblk, _ = sq.shape
+    NR, NB = R.shape[1], R.shape[2]
+    cap = min(cap, nblk)
+    kb = np.einsum("bns,src->bnrc", sk, R).argmax(-1)
+    qb = np.einsum("bns,src->bnrc", sq, R).argmax(-1)
+    cand = np.concatenate([bucket_members(kb[..., r], NB, cap)[np.arange(B)[:, None], qb[..., r]]
+                           for r in range(NR)], -1)                      # (B, nblk, P)
+    P = cand.shape[-1]
+    cc = np.maximum(cand, 0)
+    rows = np.arange(nblk)[None, :, None]
+    ok = cand >= 0
+    for p in range(1, P):
+        ok[..., p] &= ~(cc[..., :p] == cc[..., p:p + 1]).any(-1)
+    ok &= cand != rows
+    if causal:
+        ok &= cand < rows
+    sc = np.where(ok, scale * np.einsum("bis,bips->bip", sq, sk[np.arange(B)[:, None, None], cc]), -np.inf)
+    kk_c = min(topk, max(1, nblk - 1))
+    order = np.argsort(-sc, axis=-1, kind="stable")[..., :min(kk_c, P)]
+    topv = np.take_along_axis(sc, order, -1)
+    picks = np.where(np.isfinite(topv), np.take_along_axis(cc, order, -1), -1)
+    own_sc = scale * (sq * sk).sum(-1)[..., None]
+    slots = np.concatenate([np.broadcast_to(rows, (B, nblk, 1)), picks], -1)
+    return slots, np.concatenate([own_sc, np.where(np.isfinite(topv), topv, 0.0)], -1)
+
+
+def lsh_dense(sq, sk, scale, causal, topk):
+    """``LSHBucketSSA`` train-time dense selection (``src/ssa_model.py:397-405``):
+    top-k of scale * sq.sk^T over j != i (and j < i when causal), own first,
+    -inf picks invalid (-1). Returns (slots, scores) like ``lsh_route``."""
+    sq, sk = np.asarray(sq, dtype=np.float64), np.asarray(sk, dtype=np.float64)
+    B, nblk, _ = sq.shape
+    raw = scale * np.einsum("bis,bjs->bij", sq, sk)
+    j = np.arange(nblk)
+    bad = j[None, :] == j[:, None]
+    if causal:
+        bad |= j[None, :] > j[:, None]
+    raw = np.where(bad[None], -np.inf, raw)
+    kk_c = min(topk, max(1, nblk - 1))
+    order = np.argsort(-raw, axis=-1, kind="stable")[..., :kk_c]
+    topv = np.take_along_axis(raw, order, -1)
+    picks = np.where(np.isfinite(topv), order, -1)
+    own_sc = scale * (sq * sk).sum(-1)[..., None]
+    slots = np.concatenate([np.broadcast_to(j[None, :, None], (B, nblk, 1)), picks], -1)
+    return slots, np.concatenate([own_sc, np.where(np.isfinite(topv), topv, 0.0)], -1)
 
 
 def near_tie_rows(score, sel_valid_sets, k_eff, valid_mask, rel=1e-6):

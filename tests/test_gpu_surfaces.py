@@ -153,6 +153,108 @@ def test_blocksparse_distill_target_matches_oracle(dtype, L, autocast):
     assert m.distill_logits.shape == tgt.shape
 
 
+def _slot_module_oracle(m, x, slots, gval, causal):
+    """Attention over routed slots on the oracle: q, k, v from the module's
+    own projection (torch); empty places (-1) removed by a -inf gate; with
+    m.gate, logsigmoid of the slot scores added; output projection in fp64."""
+    B, L, D = x.shape
+    H, dh = m.h, m.dh
+    with torch.no_grad():
+        q, k, v = (t.view(B, L, H, dh).transpose(1, 2) for t in m.qkv(x).chunk(3, -1))
+    valid = slots >= 0
+    gate = np.where(valid, 0.0, -np.inf)
+    if m.gate:
+        gate = gate + np.where(valid, -np.logaddexp(0.0, -np.asarray(gval, dtype=np.float64)), 0.0)
+    o, _ = oattn.fwd(np64(q), np64(k), np64(v), np.maximum(slots, 0)[:, None], "slot_causal" if causal else "none",
+                     gate=gate[:, None])
+    o = o.transpose(0, 2, 1, 3).reshape(B, L, D)
+    return o @ np64(m.o.weight).T + np64(m.o.bias)
+
+
+@pytest.mark.parametrize("gate,refine", [(False, None), (True, None), (True, 3)])
+def test_centroid_module_matches_oracle(gate, refine):
+    # CentroidSSA (src/ssa_model.py:204-336): O(nblk*C) routing, non-causal attention
+    from ssa_model import CentroidSSA
+    torch.manual_seed(5)
+    B, L, d, h, Bs, s = 2, 1024, 128, 2, 32, 16
+    m = CentroidSSA(d, h, block=Bs, sel_dim=s, n_centroids=6, cpq=2, cap=3, gate=gate, refine_topk=refine).to(DEV)
+    x = torch.randn(B, L, d, device=DEV)
+    _say("centroid", gate, refine)
+    with torch.no_grad():
+        out = m(x, needle_pos=torch.tensor([100, 900], device=DEV))
+        nblk = L // Bs
+        sq = m.sel_q(x).view(B, nblk, Bs, s).mean(2)
+        kf = m.sel_k(x).view(B, nblk, Bs, s)
+        sk = torch.maximum(kf.mean(2), kf.max(2).values)
+        q, k, _ = (t.view(B, L, h, d // h).transpose(1, 2) for t in m.qkv(x).chunk(3, -1))
+        qm = q.reshape(B, h, nblk, Bs, -1).mean(3).mean(1)
+        km = k.reshape(B, h, nblk, Bs, -1).mean(3).mean(1)
+    slots, qc, kc, home = osel.centroid_route(np64(sq), np64(sk), np64(m.cent), 2, 3, refine, np64(qm), np64(km))
+    gval = np.take_along_axis(qc, home[np.arange(B)[:, None], np.maximum(slots, 0).reshape(B, -1)].reshape(
+        slots.shape), 2)
+    assert_close(np64(out), _slot_module_oracle(m, x, slots, gval, False), "f32", "centroid out")
+    assert m.last_block_logits.shape == (B, nblk) and m.align_q.shape == (B, 6)
+    assert m.last_hit is not None
+
+
+def test_centroid_module_single_centroid_is_dense():
+    # the reference's exactness check (src/ssa_model.py:212): one centroid, one
+    # route, capacity >= nblk selects every block, i.e. dense non-causal attention
+    from ssa_model import CentroidSSA
+    torch.manual_seed(6)
+    m = CentroidSSA(128, 2, block=32, sel_dim=16, n_centroids=1, cpq=1, cap=64).to(DEV)
+    x = torch.randn(1, 1024, 128, device=DEV)
+    with torch.no_grad():
+        out = m(x)
+        q, k, v = (t.view(1, 1024, 2, 64).transpose(1, 2) for t in m.qkv(x).chunk(3, -1))
+        ref = m.o(F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(1, 1024, 128))
+    assert_close(np64(out), np64(ref), "f32", "centroid dense")
+
+
+@pytest.mark.parametrize("causal,gate,dense", [(False, True, False), (True, True, False), (True, False, True),
+                                               (False, True, True)])
+def test_lsh_module_matches_oracle(causal, gate, dense):
+    # LSHBucketSSA (src/ssa_model.py:339-513): bucketed (eval) or dense (train) selection
+    from ssa_model import LSHBucketSSA
+    torch.manual_seed(7)
+    B, L, d, h, Bs, s, topk = 2, 1024, 128, 2, 32, 16, 4
+    m = LSHBucketSSA(d, h, block=Bs, topk=topk, sel_dim=s, n_rounds=3, n_buckets=4, cap=4, gate=gate,
+                     causal=causal).to(DEV)
+    m.dense_select = dense
+    x = torch.randn(B, L, d, device=DEV)
+    _say("lsh", causal, gate, dense)
+    with torch.no_grad():
+        out = m(x, needle_pos=torch.tensor([50, 700], device=DEV))
+        nblk = L // Bs
+        sq = F.normalize(m.sel_q(x).view(B, nblk, Bs, s).mean(2), dim=-1)
+        kf = m.sel_k(x).view(B, nblk, Bs, s)
+        sk = F.normalize(torch.maximum(kf.mean(2), kf.max(2).values), dim=-1)
+    if dense:
+        slots, gval = osel.lsh_dense(np64(sq), np64(sk), m.scale, causal, topk)
+    else:
+        slots, gval = osel.lsh_route(np64(sq), np64(sk), np64(m.R), 4, m.scale, causal, topk)
+    assert_close(np64(out), _slot_module_oracle(m, x, slots, gval, causal), "f32", "lsh out")
+    assert m.last_block_logits.shape == (B, nblk) and m.last_hit is not None
+
+
+def test_routed_modules_train_their_selectors():
+    # gradients reach the centroids (through the gate) and the learned hash planes
+    from ssa_model import CentroidSSA, LSHBucketSSA
+    torch.manual_seed(8)
+    x = torch.randn(1, 512, 128, device=DEV)
+    c = CentroidSSA(128, 2, block=32, sel_dim=16, n_centroids=4, cpq=2, cap=4, gate=True).to(DEV)
+    c(x).square().sum().backward()
+    assert c.cent.grad is not None and c.cent.grad.abs().sum() > 0 and c.qkv.weight.grad.abs().sum() > 0
+    lsh = LSHBucketSSA(128, 2, block=32, topk=3, sel_dim=16, gate=True, causal=True, learn_hash=True).to(DEV)
+    lsh.dense_select = True
+    lsh.train()
+    out = lsh(x)
+    assert lsh.last_hash_loss is not None and torch.isfinite(lsh.last_hash_loss)
+    (out.square().sum() + lsh.last_hash_loss).backward()
+    assert lsh.R.grad is not None and lsh.R.grad.abs().sum() > 0
+    assert lsh.sel_q[0].weight.grad.abs().sum() > 0
+
+
 def test_blocksparse_gate_gradient_paths():
     # gather path (use_triton=False) trains the selector through the gate; the
     # fused op (use_triton=True) returns no gate gradient (src/triton_kernel.py:254)

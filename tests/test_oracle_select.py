@@ -356,3 +356,81 @@ def test_qmax_closed_forms():
     fut = np.arange(nblk)[None, :] > np.arange(nblk)[:, None]
     np.testing.assert_array_equal(np.where(fut, -np.inf, s2), np.where(fut, -np.inf, sq2))
     assert all(set(cand[0, 0, i].tolist()) == set(range(i + 1)) for i in range(nblk))
+
+
+# ---------------------------------------------------------------- centroid / LSH routing
+def test_bucket_members_matches_cumcount_idiom():
+    # the reference builds the buckets with one_hot + cumsum (src/ssa_model.py:269-275)
+    home = RNG.integers(0, 5, size=(3, 40))
+    for cap in (1, 3, 40):
+        ref = torch.full((3, 5, cap), -1, dtype=torch.long)
+        h = torch.from_numpy(home)
+        oh = torch.nn.functional.one_hot(h, 5)
+        within = (oh.cumsum(1) - oh).gather(2, h.unsqueeze(-1)).squeeze(-1)
+        keep = within < cap
+        bI = torch.arange(3).view(3, 1).expand(3, 40)
+        jI = torch.arange(40).view(1, 40).expand(3, 40)
+        ref[bI[keep], h[keep], within[keep]] = jI[keep]
+        np.testing.assert_array_equal(osel.bucket_members(home, 5, cap), ref.numpy())
+
+
+def test_centroid_route_closed_form_and_invariants():
+    B, nblk, s = 2, 12, 8
+    sq, sk = RNG.standard_normal((B, nblk, s)), RNG.standard_normal((B, nblk, s))
+    # one centroid, one route, capacity >= nblk: every block (the reference's exactness check)
+    slots, _, _, _ = osel.centroid_route(sq, sk, RNG.standard_normal((1, s)), 1, nblk)
+    for i in range(nblk):
+        row = slots[0, i]
+        assert row[0] == i and sorted(row[row >= 0].tolist()) == list(range(nblk))
+    cent = RNG.standard_normal((5, s))
+    slots, qc, kc, home = osel.centroid_route(sq, sk, cent, 2, 3)
+    assert slots.shape == (B, nblk, 1 + 6)
+    for b in range(B):
+        for i in range(nblk):
+            picks = slots[b, i, 1:][slots[b, i, 1:] >= 0]
+            routes = set(np.argsort(-qc[b, i])[:2].tolist())
+            assert all(home[b, j] in routes for j in picks) and i not in picks
+            assert len(set(picks.tolist())) == len(picks)
+    qm, km = RNG.standard_normal((B, nblk, 4)), RNG.standard_normal((B, nblk, 4))
+    r2, _, _, _ = osel.centroid_route(sq, sk, cent, 2, 3, refine_topk=2, qm=qm, km=km)
+    for b in range(B):
+        for i in range(nblk):
+            full = slots[b, i, 1:][slots[b, i, 1:] >= 0]
+            best = sorted(full.tolist(), key=lambda j: -(qm[b, i] @ km[b, j]))[:2]
+            got = [j for j in r2[b, i, 1:].tolist() if j >= 0]
+            assert got == best
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_lsh_routes_reduce_to_dense_and_match_torch_topk(causal):
+    B, nblk, s, topk, scale = 2, 20, 8, 4, 2.5
+    sq, sk = RNG.standard_normal((B, nblk, s)), RNG.standard_normal((B, nblk, s))
+    sq /= np.linalg.norm(sq, axis=-1, keepdims=True)
+    sk /= np.linalg.norm(sk, axis=-1, keepdims=True)
+    dense, dsc = osel.lsh_dense(sq, sk, scale, causal, topk)
+    # one round, one bucket, capacity nblk: every block is a candidate
+    slots, sc = osel.lsh_route(sq, sk, RNG.standard_normal((s, 1, 1)), nblk, scale, causal, topk)
+    np.testing.assert_array_equal(slots, dense)
+    np.testing.assert_allclose(sc, dsc, rtol=1e-12)
+    # the reference's dense top-k (src/ssa_model.py:397-405) on these tie-free scores
+    t_sq, t_sk = torch.from_numpy(sq), torch.from_numpy(sk)
+    raw = scale * (t_sq @ t_sk.transpose(-1, -2))
+    diag = torch.arange(nblk)
+    raw = raw.masked_fill(diag.view(1, nblk, 1) == diag.view(1, 1, nblk), float("-inf"))
+    if causal:
+        raw = raw.masked_fill(diag.view(1, 1, nblk) > diag.view(1, nblk, 1), float("-inf"))
+    topv, topi = raw.topk(min(topk, nblk - 1), dim=-1)
+    ref = torch.where(torch.isfinite(topv), topi, torch.full_like(topi, -1)).numpy()
+    np.testing.assert_array_equal(dense[..., 1:], ref)
+    # several rounds and buckets: picks come from the query's buckets, distinct, past only when causal
+    R = RNG.standard_normal((s, 3, 4))
+    slots, _ = osel.lsh_route(sq, sk, R, 3, scale, causal, topk)
+    kb = np.einsum("bns,src->bnrc", sk, R).argmax(-1)
+    qb = np.einsum("bns,src->bnrc", sq, R).argmax(-1)
+    for b in range(B):
+        for i in range(nblk):
+            picks = [j for j in slots[b, i, 1:].tolist() if j >= 0]
+            assert len(set(picks)) == len(picks) and i not in picks
+            assert all((kb[b, j] == qb[b, i]).any() for j in picks)
+            if causal:
+                assert all(j < i for j in picks)
