@@ -178,6 +178,20 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
     return fail(FBSA_EINVAL, "fbsa_select: misaligned pointer");
   const int64_t ntile = (d->nblk + 7) / 8;
   if (ntile * d->B * d->H > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select: grid too large");
+  // Quest scores of wide operands (D >= 128, past the MFMA engine's widths)
+  // under _finish for every row and without chosen-slot scores: the row-per-
+  // workgroup exact kernel of fbsa_select_qmax with one query vector per block
+  // (float64 scores, radix top-k; same blocks and tie-break, several times
+  // faster than the streaming fp64 kernel at these widths)
+  if (d->score == FBSA_SCORE_QUEST && d->convention == FBSA_SEL_SORTED_SINK && !sel_score && row_begin == 0 &&
+      row_end == d->nblk && d->D >= 128 && d->nblk <= 4096) {
+    fbsa_qmax_desc q = {};
+    q.dtype = d->dtype; q.convention = FBSA_SEL_SORTED_SINK; q.sink = d->sink; q.flags = FBSA_QMAX_EXACT;
+    q.B = d->B; q.H = d->H; q.nblk = d->nblk; q.D = d->D; q.tok = 1; q.la = d->nblk;
+    q.topk = d->topk; q.kk = d->kk; q.ncand = 0;
+    if (!aligned(a, 16)) return fail(FBSA_EINVAL, "fbsa_select: misaligned pointer");
+    return run_select_qmax(&q, a, b1, b2, nullptr, sel, nullptr, (hipStream_t)stream);
+  }
   // the workspace enables the MFMA path; without one the fp64 kernel runs (same results)
   const size_t need = select_workspace_bytes(d);
   void *ws = (workspace && workspace_bytes >= need && need > 0) ? workspace : nullptr;

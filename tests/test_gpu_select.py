@@ -108,6 +108,31 @@ def test_select_quest_config4_shape(dtype, engine):
     _check_sel(idx, ref, "idx")
 
 
+@pytest.mark.parametrize("D,ties,sink,topk", [(128, False, True, 8), (256, True, True, 62), (128, True, False, 30),
+                                               (256, False, False, 16)])
+def test_select_quest_wide_rows(D, ties, sink, topk):
+    # Quest + _finish at D >= 128 without chosen-slot scores runs on the row-per-
+    # workgroup exact kernel; with scores requested, on the streaming fp64 kernel:
+    # both must give the oracle's blocks
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(9)
+    B, H, nblk = 1, 2, 700
+    if ties:
+        mk = lambda: torch.randint(-2, 3, (B, H, nblk, D), generator=g).to(torch.bfloat16)  # noqa: E731
+    else:
+        mk = lambda: randn(g, (B, H, nblk, D), "bf16")  # noqa: E731
+    a, b1, b2 = mk(), mk(), mk()
+    b1, b2 = torch.maximum(b1, b2), torch.minimum(b1, b2)
+    _say("quest wide", D, ties, sink, topk)
+    kw = dict(score="quest", convention="sorted_sink", topk=topk, sink=sink)
+    sel = selection.select(a.to(DEV), b1.to(DEV), b2.to(DEV), **kw)
+    sel2, _ = selection.select(a.to(DEV), b1.to(DEV), b2.to(DEV), need_scores=True, **kw)
+    raw = osel.scores(np64(a), np64(b1), "bf16", "quest", b2=np64(b2))
+    ref = osel.select_conv_b(raw, topk, sink)
+    _check_sel(sel.cpu().numpy(), ref, "sel (row kernel)")
+    _check_sel(sel2.cpu().numpy(), ref, "sel (streaming kernel)")
+
+
 @pytest.mark.parametrize("engine", ["auto", "fp64"])
 def test_select_max2_module_scores(engine):
     # BlockSparseSSA._scores: max(sq . sk_mean, sq . sk_max) (src/ssa_model.py:113-119)
