@@ -67,9 +67,12 @@ struct QmaxArgs {
 };
 
 // Orderable key of a score: larger scores give larger keys; -0 and +0 share
-// one key (torch compares them equal, so the lower index wins their tie).
+// one key (torch compares them equal, so the lower index wins their tie); any
+// NaN becomes the positive quiet NaN, whose key is the largest (torch.topk
+// ranks NaN first) and, like every grid value's, has zero low bits.
 __device__ __forceinline__ uint32_t qm_key(float v) {
   if (v == 0.f) v = 0.f;
+  if (v != v) v = __uint_as_float(0x7FC00000u);
   const uint32_t u = __float_as_uint(v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }

@@ -121,6 +121,34 @@ def test_select_qmax_candidate_list_rules():
     np.testing.assert_array_equal(got, osel.select_conv_b(sc, topk, True))
 
 
+@pytest.mark.parametrize("two_stage", [False, True])
+def test_select_qmax_f16_overflow(two_stage):
+    # fp16 scores past 65504 round to inf (and inf - inf to NaN), as torch's fp16
+    # einsums make them; NaN ranks first and non-finite picks become the own block
+    from fbsa_amd import selection
+    q, k = _inputs(47, 1, 4, 2, 2048, 128, "f16")
+    # every third key block large (its scores overflow to inf), block 7 large
+    # and positive (its min is large too: inf - inf = NaN), the rest moderate
+    kf = k.float().view(1, 2, 32, 64, 128)
+    scale = torch.full((32,), 8.0)
+    scale[::3] = 30.0
+    kf = kf * scale.view(1, 1, 32, 1, 1)
+    kf[:, :, 7] = kf[:, :, 7].abs() + 100
+    q, k = (q.float() * 16).half(), kf.view(1, 2, 2048, 128).half()
+    if two_stage:
+        ref, sc, _ = osel.select_two_stage(np64(q), np64(k), 64, 5, True, 2, "f16")
+    else:
+        ref, sc = osel.select_quest_qmax(np64(q), np64(k), 64, 5, True, "f16")
+    past = np.arange(32)[None, :] <= np.arange(32)[:, None]
+    assert np.isinf(sc[..., past]).any() and np.isnan(sc[..., past]).any() and np.isfinite(sc[..., past]).any()
+    for engine in ("auto", "fp64"):
+        _say("f16 overflow", two_stage, engine)
+        fn = selection.select_two_stage if two_stage else selection.select_quest_qmax
+        kw = dict(over=2) if two_stage else {}
+        got = fn(q.to(DEV), k.to(DEV), 64, 5, sink=True, engine=engine, **kw)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
 def test_select_qmax_full_qwen_shape_properties():
     # configuration-4 shape (L 65536, Hq 16, Hkv 2, D 256, bs 128, top-32): the
     # two engines agree, and rows of a causal prefix do not depend on the rest
