@@ -45,6 +45,8 @@ def parse():
     p.add_argument("--bs", type=int, default=64)
     p.add_argument("--topk", type=int, default=16)
     p.add_argument("--bwd", action="store_true", help="also time the backward (separate fields)")
+    p.add_argument("--graph", action="store_true",
+                   help="time the step as one replayed HIP graph (fbsa_amd.pipeline.GraphStep)")
     p.add_argument("--overlap", action="store_true",
                    help="time the two-stream step (selection overlapped with the forward)")
     p.add_argument("--splits", type=int, default=4, help="row ranges of the overlapped step")
@@ -279,7 +281,11 @@ def main():
             fwd_ms.append((e1, e2))
         return sel, o, lse
 
+    graph = pipeline.GraphStep(q, k, v, bs, topk, need_lse=True) if a.graph else None
+
     def step():
+        if graph is not None:
+            return graph.replay()
         if not a.overlap:
             return seq_step(False)
         return pipeline.select_and_attend(q, k, v, bs, topk, need_lse=True, splits=a.splits)
@@ -322,6 +328,7 @@ def main():
                                "own-first) + fused block-sparse forward, causal",
                    "B": B, "H": H, "N": N, "D": D, "block": bs, "nblk": nblk, "topk": topk, "kk": kk,
                    "step": (f"selection overlapped with the forward ({a.splits} row ranges, 2 streams)" if a.overlap
+                            else "pool, select, forward in sequence, replayed as one HIP graph" if a.graph
                             else "pool, select, forward in sequence on one stream")},
         "ms_select": t_sel, "ms_fwd": t_fwd,
         "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,

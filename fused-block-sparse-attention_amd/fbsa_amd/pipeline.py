@@ -72,3 +72,42 @@ def select_and_attend(q, k, v, bs, topk, *, causal=True, scale=None, need_lse=Fa
     if need_lse:
         return sel[:, 0], out[0], out[1]
     return sel[:, 0], out
+
+
+class GraphStep:
+    """The sequential select + forward step recorded once as a HIP graph and
+    replayed, for loops that repeat the step on fixed buffers (serving,
+    benchmarks): pool q and k, the top-k selection and the fused forward go
+    out as one graph launch instead of one host launch each.
+
+    The step runs eagerly ``warmup`` times on a side stream (first-use setup
+    such as kernel attributes happens there), then is captured with its
+    workspaces in a graph-private memory pool. ``replay()`` re-runs it on the
+    same q, k, v tensors (update them in place between replays) and returns
+    the same output tensors (sel (B, nblk, kk) int32, o[, lse]), overwritten.
+    None of the step's launches is a memset, so every replay is
+    self-contained. Same values as ``selection.select_mean_pooled`` followed
+    by ``ops.attention_forward``.
+    """
+
+    def __init__(self, q, k, v, bs, topk, *, causal=True, scale=None, need_lse=False, engine="auto", warmup=2):
+        mask = ops.MASK_SLOT_CAUSAL if causal else ops.MASK_NONE
+
+        def run():
+            sel = selection.select_mean_pooled(q, k, bs, topk, causal=causal, engine=engine)
+            out = ops.attention_forward(q, k, v, sel[:, None], mask=mask, scale=scale, need_lse=need_lse)
+            return (sel,) + (tuple(out) if need_lse else (out,))
+
+        side = torch.cuda.Stream(device=q.device)  # default priority
+        side.wait_stream(torch.cuda.current_stream(q.device))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                run()
+        torch.cuda.current_stream(q.device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.outputs = run()
+
+    def replay(self):
+        self.graph.replay()
+        return self.outputs

@@ -74,3 +74,34 @@ def test_pipelined_step_equals_sequential(N, splits):
     torch.cuda.synchronize()
     assert torch.equal(psel2, sel) and torch.equal(po2, o)
 
+
+
+@pytest.mark.parametrize("engine,need_lse", [("auto", True), ("fp64", False)])
+def test_graph_step_replays_match_eager(engine, need_lse):
+    # the captured step, replayed several times with eager work and
+    # synchronisations in between, equals the eager step every time, also
+    # after the inputs change in place
+    from fbsa_amd import ops, pipeline, selection
+    g = torch.Generator().manual_seed(12)
+    B, H, L, D, bs, topk = 1, 4, 16384, 64, 64, 16
+    q, k, v = (randn(g, (B, H, L, D), "bf16", scale=0.125).to(DEV) for _ in range(3))
+
+    def eager():
+        sel = selection.select_mean_pooled(q, k, bs, topk, causal=True, engine=engine)
+        out = ops.attention_forward(q, k, v, sel[:, None], mask=ops.MASK_SLOT_CAUSAL, need_lse=need_lse)
+        return (sel,) + (tuple(out) if need_lse else (out,))
+
+    _say("graph step", engine, need_lse)
+    step = pipeline.GraphStep(q, k, v, bs, topk, need_lse=need_lse, engine=engine)
+    for rep in range(4):
+        if rep == 2:  # new inputs, same buffers
+            q.copy_(randn(g, (B, H, L, D), "bf16", scale=0.125).to(DEV))
+            v.mul_(-1)
+        got = [t.clone() for t in step.replay()]
+        torch.cuda.synchronize()
+        ref = eager()
+        x = torch.randn(1000, device=DEV).sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(x)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b), f"replay {rep}"
