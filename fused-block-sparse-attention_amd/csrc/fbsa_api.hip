@@ -218,7 +218,8 @@ int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, con
   if (d->nblk > 65536) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: nblk %lld > 65536", (long long)d->nblk);
   if (cand && d->ncand < 1) return fail(FBSA_EINVAL, "fbsa_select_qmax: ncand must be >= 1 with a candidate list");
   const int64_t ncol = cand ? d->ncand : d->nblk;
-  if (ncol > 4096) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: %lld columns per row > 4096", (long long)ncol);
+  // two 32-bit keys and two 16-bit indices per column in LDS, beside the tile ring
+  if (ncol > 8192) return fail(FBSA_EUNSUPPORTED, "fbsa_select_qmax: %lld columns per row > 8192", (long long)ncol);
   const int64_t K = d->topk < d->nblk ? d->topk : d->nblk;
   const int64_t kk = d->convention == FBSA_SEL_SORTED_SINK ? K + 1 + (d->sink ? 1 : 0) : K;
   if (kk < 1) return fail(FBSA_EINVAL, "fbsa_select_qmax: SORTED_TOPK needs topk >= 1");

@@ -187,7 +187,7 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
  * fbsa_select_qmax_workspace_bytes() bytes (16-byte aligned; it holds the
  * key-block norms) bracket the scores on MFMA and compute exactly (float64)
  * only the scores the top-k needs; other cases, no workspace, or
- * FBSA_QMAX_EXACT compute every score in float64; all give the same result. Supports D in {32,64,128,256}, nblk <= 65536 and at most 4096
+ * FBSA_QMAX_EXACT compute every score in float64; all give the same result. Supports D in {32,64,128,256}, nblk <= 65536 and at most 8192
  * columns per row (nblk, or ncand with a candidate list). Replaces
  * SelectMaxQMax.select (tok = bs, a = the GQA-group mean of every token;
  * src/qwen_blocksparse.py:216-241) and both stages of SelectTwoStage

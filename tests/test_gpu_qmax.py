@@ -178,3 +178,27 @@ def test_select_qmax_full_qwen_shape_properties():
     assert torch.equal(t, t64)
     # the first over*topk rows have every past block as a candidate
     assert torch.equal(t[:, :, :4 * topk], a[:, :, :4 * topk])
+
+
+def test_select_qmax_8192_columns():
+    # the largest row the kernel takes (nblk 8192: 1M tokens at block 128, here
+    # 512K at block 64): rows of the 262144-token prefix match the prefix run,
+    # and sampled late rows match the oracle row by row
+    from fbsa_amd import selection
+    g = torch.Generator(device=DEV).manual_seed(48)
+    B, Hq, Hkv, L, D, bs, topk = 1, 2, 1, 524288, 64, 64, 16
+    q = torch.randn(B, Hq, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=g, device=DEV).to(torch.bfloat16)
+    _say("8192 columns")
+    full = selection.select_quest_qmax(q, k, bs, topk)
+    n = 262144
+    pre = selection.select_quest_qmax(q[:, :, :n].contiguous(), k[:, :, :n].contiguous(), bs, topk)
+    assert torch.equal(full[:, :, :n // bs], pre)
+    qg = np64(selection.pool(q, 1, "mean_grp_then_tok", grp=2))
+    kmin, kmax = (np64(t) for t in selection.pool(k, bs, "minmax"))
+    got = full.cpu().numpy()
+    for i in (4096, 6000, 8191):
+        tok = osel.scores(qg[:, :, i * bs:(i + 1) * bs], kmax, "bf16", "quest", b2=kmin)  # (B,H,bs,nblk)
+        row = tok.max(axis=2)[:, :, None, :]
+        ref = osel.select_conv_b(row, topk, True, rows=[i])
+        np.testing.assert_array_equal(got[:, :, i:i + 1], ref)
