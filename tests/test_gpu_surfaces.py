@@ -459,3 +459,75 @@ def test_qwen_block_mass_matches_oracle(dtype, L, d, bs):
     idx = SelectOracle(topk=topk, bs=bs, sink=True, mass=got).select(None, None).cpu().numpy()
     ridx = osel.select_conv_b(ref, topk, True)
     assert (idx == ridx).all(-1).mean() > 0.97  # rows apart only at near-equal masses
+
+
+@pytest.mark.parametrize("which", ["ssa", "lsh", "lsh_dense", "qwen"])
+def test_causal_modules_do_not_leak(which):
+    # src/check_lsh_causal.py: perturbing the inputs from block p on must leave
+    # every output before position p unchanged (here: bit for bit)
+    from ssa_model import BlockSparseSSA, LSHBucketSSA
+    from qwen_blocksparse import SelectMax, blocksparse_forward
+    torch.manual_seed(9)
+    d, h, B, L, block = 128, 4, 2, 1024, 32
+    if which == "qwen":
+        q, k, v = (torch.randn(B, s, L, 64, device=DEV, dtype=torch.bfloat16) for s in (8, 2, 2))
+
+        def run(qq, kk_, vv):
+            return blocksparse_forward(qq, kk_, vv, selector=SelectMax(topk=4, bs=block), topk=4, bs=block)
+    else:
+        m = (BlockSparseSSA(d, h, block=block, topk=4, causal=True, gate=True) if which == "ssa" else
+             LSHBucketSSA(d, h, block=block, topk=4, causal=True, gate=True)).to(DEV).eval()
+        m.dense_select = which == "lsh_dense"
+        x = torch.randn(B, L, d, device=DEV)
+    for pb in (L // block - 1, L // block // 2, 3):
+        p = pb * block
+        _say("leak", which, pb)
+        with torch.no_grad():
+            if which == "qwen":
+                o1 = run(q, k, v)
+                q2, k2, v2 = q.clone(), k.clone(), v.clone()
+                for t in (q2, k2, v2):
+                    t[:, :, p:] += 3.0
+                o2 = run(q2, k2, v2)
+                before, after = o1[:, :, :p], o2[:, :, :p]
+                changed = (o1[:, :, p:] - o2[:, :, p:]).abs().max()
+            else:
+                o1 = m(x)
+                x2 = x.clone()
+                x2[:, p:] += 10.0
+                o2 = m(x2)
+                before, after = o1[:, :p], o2[:, :p]
+                changed = (o1[:, p:] - o2[:, p:]).abs().max()
+        assert torch.equal(before, after), f"{which}: outputs before block {pb} changed"
+        assert changed > 0
+
+
+def test_blocksparse_module_large_nblk():
+    # src/verify_kernel.py's large case: d64 h2 L=1,120,000 block 16 -> nblk 70000
+    # (> 65535), top-2, causal, gated, bf16; sampled query blocks against the oracle
+    from ssa_model import BlockSparseSSA
+    from oracle.numerics import round_to
+    torch.manual_seed(0)
+    d, h, B, L, Bs, topk = 64, 2, 1, 70000 * 16, 16, 2
+    m = BlockSparseSSA(d, h, block=Bs, topk=topk, causal=True, gate=True).to(DEV).to(torch.bfloat16).eval()
+    x = torch.randn(B, L, d, device=DEV, dtype=torch.bfloat16)
+    nblk, dh = L // Bs, d // h
+    _say("large nblk")
+    with torch.no_grad():
+        out = m(x)
+        q, k, v = (t.view(B, L, h, dh).transpose(1, 2) for t in m.qkv(x).chunk(3, -1))
+        sq, skm, skx = m._pooled(x, B, nblk, Bs)
+    assert torch.isfinite(out.float()).all()
+    rows = np.array([0, 1, 2, 5, 65534, 65535, 65536, 69999])
+    raw = osel.scores(np64(sq), np64(skm), "bf16", "max2", b2=np64(skx), rows=rows)   # (B, R, nblk)
+    sel_r = osel.select_conv_a(raw, topk, True, rows=rows)                              # (B, R, kk)
+    gate_r = round_to(osel.gate_from_scores(raw, sel_r), "bf16")
+    kk = sel_r.shape[-1]
+    sel = np.tile(np.arange(nblk)[None, :, None], (B, 1, kk))
+    gate = np.zeros((B, nblk, kk))
+    sel[:, rows], gate[:, rows] = sel_r, gate_r
+    o, _ = oattn.fwd(np64(q), np64(k), np64(v), sel[:, None], "slot_causal", gate=gate[:, None], rows=rows)
+    o = o.reshape(B, h, len(rows), Bs, dh).transpose(0, 2, 3, 1, 4).reshape(B, len(rows) * Bs, d)
+    ref = o @ np64(m.o.weight).T + np64(m.o.bias)
+    pos = (rows[:, None] * Bs + np.arange(Bs)[None, :]).ravel()
+    assert_close(np64(out[:, pos]), ref, "bf16", "large-nblk out")
