@@ -263,9 +263,11 @@ struct BwdArgs {
   int mask, grp;
 };
 
-template <typename T, int BS, int D, int BUDGET, int META> struct BwdCfg {
+// ROWS: the block rows one workgroup owns (one wave per 16), BS unless a
+// block is split over several workgroups.
+template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct BwdCfg {
   static constexpr int ES = sizeof(T);
-  static constexpr int NW = BS / 16;
+  static constexpr int NW = ROWS / 16;
   static constexpr int NT = NW * 64;
   static constexpr int KC = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
   static constexpr int NCH = BS / KC;
@@ -368,6 +370,11 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int c = 0; c < C::NSTAGE - 1; ++c)
     if (c < nchunks) issue(c);
+  // the register-operand loads above and the first stages have landed (issued
+  // together, so their latencies overlap): the compiler then waits for nothing
+  // inside the ring loop, where its own waits would also drain the prefetch
+  wait_vmcnt<0>();
+
 
   for (int c = 0; c < nchunks; ++c) {
     // stage c has landed for this wave (up to NSTAGE - 2 later stages may be in flight);
@@ -442,13 +449,35 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   }
 }
 
+// A dK/dV wave keeps its 16 keys' K and V fragments and their dK and dV
+// accumulators in registers: 2 D (16-bit) or 4 D (fp32) values per lane besides
+// the per-chunk S, dP and tile reads. Eight waves (bs 128) share a SIMD two by
+// two, leaving 256 registers each, too few from 16-bit d 256 or fp32 d 128 on
+// (the remainder went to scratch); there a workgroup takes half a key block (four
+// waves, one per SIMD, 512 registers each) and the two halves of a block run
+// next to each other on one XCD, so the second read of each Q / dO tile is an L2
+// hit. Such a workgroup holds a whole CU's registers, so its ring can take
+// most of the LDS.
+template <typename T, int D> constexpr bool dkdv_heavy() { return D >= 256 || (sizeof(T) == 4 && D >= 128); }
+template <typename T, int BS, int D> constexpr int dkdv_rows() { return BS == 128 && dkdv_heavy<T, D>() ? 64 : BS; }
+#ifndef FBSA_DKDV_HEAVY_LDS_BUDGET
+#define FBSA_DKDV_HEAVY_LDS_BUDGET 102400
+#endif
+template <typename T, int BS, int D>
+using DkdvCfg = BwdCfg<T, BS, D,
+                       dkdv_heavy<T, D>() && dkdv_rows<T, BS, D>() == 64 ? FBSA_DKDV_HEAVY_LDS_BUDGET
+                                                                        : FBSA_DKDV_LDS_BUDGET,
+                       1, dkdv_rows<T, BS, D>()>;
+
 // Latency bound (each chunk is a short chain of LDS reads, MFMAs and
 // exponentials), so occupancy decides: for bs 64 with 16-bit d <= 64 the
 // kernel is held to four waves per SIMD (at most 128 VGPRs) and its two-stage
 // ring (35 KB of LDS) fits four workgroups per CU.
 template <typename T, int BS, int D>
-__global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4 : 1) void dkdv_kernel(BwdArgs a) {
-  using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
+__global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4 : 1) void
+dkdv_kernel(BwdArgs a) {
+  using C = DkdvCfg<T, BS, D>;
+  constexpr int NPART = BS / C::NW / 16;  // workgroups per key block
   constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
   constexpr int HR = C::KC >= 64 ? 32 : C::KC;  // query rows per part of a chunk
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -456,8 +485,9 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4
   int4 *s_meta = (int4 *)(smem + C::NSTAGE * C::STAGE_BYTES);  // per entry: query block, mask kind, gate bits
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
-  const int64_t total = a.B * a.Hkv * a.nblk;
+  const int64_t total = a.B * a.Hkv * a.nblk * NPART;
   int64_t t = xcd_remap(blockIdx.x, total);
+  const int kpart = (int)(t % NPART); t /= NPART;
   const int64_t j = t % a.nblk; t /= a.nblk;
   const int hk = (int)(t % a.Hkv);
   const int64_t b = t / a.Hkv;
@@ -465,7 +495,7 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4
   const int64_t seg = (b * a.hsel + hs) * a.nblk + j;
   const int e0 = a.seg_off[seg], e1 = a.seg_off[seg + 1];
 
-  const int u = w * 16 + p;  // this lane's key row within block j (B-operand column)
+  const int u = kpart * C::NW * 16 + w * 16 + p;  // this lane's key row within block j (B-operand column)
   const int64_t kpos = j * BS + u;
   RowFrag<T, D> kf, vf;
   kf.load((const T *)a.k + b * a.sk[0] + hk * a.sk[1] + kpos * a.sk[2], g);
@@ -535,6 +565,11 @@ __global__ __launch_bounds__(BS * 4, (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4
 #pragma unroll
     for (int c = 0; c < C::NSTAGE - 1; ++c)
       if (c < nchunks) issue();
+    // the register-operand loads above and the first stages have landed (issued
+    // together, so their latencies overlap): the compiler then waits for nothing
+    // inside the ring loop, where its own waits would also drain the prefetch
+    wait_vmcnt<0>();
+
 
     int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
     for (int c = 0; c < nchunks; ++c) {
@@ -679,12 +714,13 @@ template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipS
 }
 
 template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
-  using C = BwdCfg<T, BS, D, FBSA_DKDV_LDS_BUDGET, 1>;
+  using C = DkdvCfg<T, BS, D>;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16;
   static size_t granted = 0;
   int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
   if (e) return e;
-  hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)(a.B * a.Hkv * a.nblk)), dim3(C::NT), lds, s, a);
+  const int64_t nwg = a.B * a.Hkv * a.nblk * (BS / (C::NW * 16));
+  hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dkdv_kernel launch");
 }
 

@@ -40,11 +40,30 @@ __host__ __device__ constexpr int swz(int row, int cpr) {
 }
 
 // ---- gfx950 primitives ----------------------------------------------------
-// 16-byte global -> LDS copy: lane l's bytes land at lds_wave_base + 16*l.
+// Direct-to-LDS global loads (global_load_lds, LDS destination in M0):
+// lane l's 4 or 16 bytes land at lds_wave_base + 4*l or + 16*l, the base
+// wave-uniform. They are issued by inline asm because the compiler's wait
+// insertion cannot tell the LDS they write from any LDS a later ordinary load
+// reads: it waits for vmcnt(0) there, which also waits for the ring stages just
+// prefetched and so takes away the overlap the ring exists for. Every consumer
+// waits for its stage itself (wait_vmcnt / wait_ring, then lds_barrier() or
+// __syncthreads()); the "memory" clobber keeps LDS accesses from moving across
+// an issue. Waits the compiler inserts for its own loads stay correct (loads
+// leave vmcnt in issue order, so uncounted DMA only makes them wait longer).
+// M0 is written here without being preserved: these two are the only code in
+// the library that uses M0 (no LDS-DMA builtin, message, GWS or indexed
+// register move), so no value of the compiler's lives in it across the asm.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void g2lds16(const void *gsrc, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
-                                   (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(m) : "memory", "m0");
 }
+__device__ __forceinline__ void g2lds4(const void *gsrc, void *lds_wave_base) {
+  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gsrc), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0] at bits 3:0, vmcnt[5:4] at bits 15:14, expcnt/lgkmcnt left open).

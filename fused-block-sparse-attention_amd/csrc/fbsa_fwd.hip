@@ -195,6 +195,11 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int c = 0; c < C::NSTAGE - 1; ++c)
     if (c < nchunks) issue(c);
+  // the register-operand loads above and the first stages have landed (issued
+  // together, so their latencies overlap): the compiler then waits for nothing
+  // inside the ring loop, where its own waits would also drain the prefetch
+  wait_vmcnt<0>();
+
 
   for (int c = 0; c < nchunks; ++c) {
     // chunk c has landed once at most min(ahead, NSTAGE-2) later chunks are in flight

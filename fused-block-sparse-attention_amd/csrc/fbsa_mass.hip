@@ -94,6 +94,11 @@ __global__ __launch_bounds__(BS * 4) void mass_kernel(MassArgs a) {
 #pragma unroll
   for (int c = 0; c < C::NSTAGE - 1; ++c)
     if (c < nchunks) issue(c);
+  // the register-operand loads above and the first stages have landed (issued
+  // together, so their latencies overlap): the compiler then waits for nothing
+  // inside the ring loop, where its own waits would also drain the prefetch
+  wait_vmcnt<0>();
+
 
   float mx = -INFINITY, sm = 0.f;  // pass 1: this lane's running max and sum
   float acc = 0.f;                 // pass 2: this lane's sum over the current key block

@@ -280,12 +280,6 @@ template <int D> struct QmCfg {
   static constexpr int NSTAGE = 3;
 };
 
-// 4-byte global -> LDS copy: lane l's word lands at lds_wave_base + 4*l.
-__device__ __forceinline__ void g2lds4(const void *gsrc, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
-                                   (__attribute__((address_space(3))) void *)lds_wave_base, 4, 0, 0);
-}
-
 // Dynamic LDS: s_lo, s_hi (u32) and s_col, s_cl (u16), ncolp entries each,
 // then the tile ring (bracket pass only).
 template <int D, int TOK> static size_t qm_lds_bytes(int64_t ncolp) {

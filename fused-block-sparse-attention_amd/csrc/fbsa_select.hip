@@ -1160,6 +1160,11 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
 #pragma unroll
   for (int k = 0; k < NST - 1; ++k)
     if (k < 2 * nt) issue(tile_of(k), k);
+  // the register-operand loads above and the first stages have landed (issued
+  // together, so their latencies overlap): the compiler then waits for nothing
+  // inside the ring loop, where its own waits would also drain the prefetch
+  wait_vmcnt<0>();
+
 
   // one ring step: wait for stage it, refill, score its tile (lo in pass 1, hi in pass 2)
   auto step = [&](int it, auto masked_c, auto collect_c) {

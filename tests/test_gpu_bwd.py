@@ -94,10 +94,11 @@ def test_block_and_head_sizes_random_sel_with_duplicates(bs, D):
     _cmp(got, _oracle(q, k, v, sel, do, "slot_causal"), "bf16")
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_gqa_token_causal_padding_outgate(dtype):
+@pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f32", 128), ("bf16", 256), ("f16", 256)])
+def test_gqa_token_causal_padding_outgate(dtype, D):
+    # bs 128 with fp32 d 128 or 16-bit d 256 splits each key block's dK/dV over two workgroups
     g = torch.Generator().manual_seed(3)
-    B, Hq, Hkv, N, D, bs, topk = 1, 8, 2, 1024, 128, 128, 3
+    B, Hq, Hkv, N, bs, topk = 1, 8, 2, 1024, 128, 3
     q, do, og = (randn(g, (B, Hq, N, D), dtype) for _ in range(3))
     k, v = (randn(g, (B, Hkv, N, D), dtype) for _ in range(2))
     idx, _ = osel.select_quest(np64(q), np64(k), bs, topk, True, dtype)
