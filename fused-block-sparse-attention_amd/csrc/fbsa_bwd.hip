@@ -455,18 +455,36 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 // two, leaving 256 registers each, too few from 16-bit d 256 or fp32 d 128 on
 // (the remainder went to scratch); there a workgroup takes half a key block (four
 // waves, one per SIMD, 512 registers each) and the two halves of a block run
-// next to each other on one XCD, so the second read of each Q / dO tile is an L2
-// hit. Such a workgroup holds a whole CU's registers, so its ring can take
+// back to back on one XCD, so the second read of each Q / dO tile is an L2 hit. Such a workgroup holds a whole CU's registers, so its ring can take
 // most of the LDS.
+// For 16-bit d 256 the keys' work is split over two waves by role instead: wave
+// 0 of a pair holds K, forms S and P and accumulates dV; wave 1 holds V, forms
+// dP, takes P from its partner through LDS and accumulates dK. Each wave then
+// holds one fragment and one accumulator (half the registers), two waves share
+// each SIMD, and the MFMA and LDS work per key is unchanged; P and dS are the
+// same expressions in the same order, so results do not change.
 template <typename T, int D> constexpr bool dkdv_heavy() { return D >= 256 || (sizeof(T) == 4 && D >= 128); }
-template <typename T, int BS, int D> constexpr int dkdv_rows() { return BS == 128 && dkdv_heavy<T, D>() ? 64 : BS; }
+template <typename T, int D> constexpr int dkdv_roles() { return sizeof(T) == 2 && D >= 256 ? 2 : 1; }
+template <typename T, int BS, int D> constexpr int dkdv_keys() {  // keys per workgroup
+  return dkdv_roles<T, D>() == 2 ? (BS < 64 ? BS : 64) : (BS == 128 && dkdv_heavy<T, D>() ? 64 : BS);
+}
+template <typename T, int BS, int D> constexpr int dkdv_rows() { return dkdv_keys<T, BS, D>() * dkdv_roles<T, D>(); }
+// Minimum resident workgroups for the register budget; the compiler counts a
+// workgroup as at least one wave per SIMD, so 2 means two waves per SIMD for
+// workgroups of up to four waves, and 1 does for eight-wave workgroups.
+template <typename T, int BS, int D> constexpr int dkdv_minwg() {
+  return dkdv_roles<T, D>() == 2 ? (dkdv_rows<T, BS, D>() >= 128 ? 1 : 2)
+                                 : (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4 : 1;
+}
 #ifndef FBSA_DKDV_HEAVY_LDS_BUDGET
 #define FBSA_DKDV_HEAVY_LDS_BUDGET 102400
 #endif
 template <typename T, int BS, int D>
 using DkdvCfg = BwdCfg<T, BS, D,
-                       dkdv_heavy<T, D>() && dkdv_rows<T, BS, D>() == 64 ? FBSA_DKDV_HEAVY_LDS_BUDGET
-                                                                        : FBSA_DKDV_LDS_BUDGET,
+                       dkdv_heavy<T, D>() && (dkdv_roles<T, D>() == 2 ? dkdv_rows<T, BS, D>() >= 64
+                                                                     : dkdv_rows<T, BS, D>() == 64)
+                           ? FBSA_DKDV_HEAVY_LDS_BUDGET / dkdv_minwg<T, BS, D>()
+                           : FBSA_DKDV_LDS_BUDGET,
                        1, dkdv_rows<T, BS, D>()>;
 
 // Latency bound (each chunk is a short chain of LDS reads, MFMAs and
@@ -474,20 +492,35 @@ using DkdvCfg = BwdCfg<T, BS, D,
 // kernel is held to four waves per SIMD (at most 128 VGPRs) and its two-stage
 // ring (35 KB of LDS) fits four workgroups per CU.
 template <typename T, int BS, int D>
-__global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (BS == 64 && D <= 64 && sizeof(T) == 2) ? 4 : 1) void
-dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>())) void dkdv_kernel(BwdArgs a) {
   using C = DkdvCfg<T, BS, D>;
-  constexpr int NPART = BS / C::NW / 16;  // workgroups per key block
+  constexpr int ROLES = dkdv_roles<T, D>(), KEYS = dkdv_keys<T, BS, D>();
+  constexpr int NPART = BS / KEYS;  // workgroups per key block
   constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
   constexpr int HR = C::KC >= 64 ? 32 : C::KC;  // query rows per part of a chunk
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
   int4 *s_meta = (int4 *)(smem + C::NSTAGE * C::STAGE_BYTES);  // per entry: query block, mask kind, gate bits
+  float4 *s_xch = (float4 *)(s_meta + MAXE);  // two roles: P of each key group's part, [KEYS/16][64 lanes][HR/16]
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
-  const int64_t total = a.B * a.Hkv * a.nblk * NPART;
-  int64_t t = xcd_remap(blockIdx.x, total);
-  const int kpart = (int)(t % NPART); t /= NPART;
+  // Launch order. Causal selection gives low key blocks far longer transposed
+  // lists than high ones. When every XCD's contiguous share of the (b, KV head,
+  // block) units is whole rows of key blocks, the shares carry equal work and
+  // neighbouring blocks (read by overlapping query blocks) share an L2: XCD-
+  // contiguous ranges. Otherwise (a share is part of a row) such ranges would
+  // leave most of the work on a few XCDs: units go round-robin over the XCDs
+  // instead. Either way a block's NPART workgroups run back to back on one XCD.
+  const int64_t nunits = a.B * a.Hkv * a.nblk;
+  int kpart = 0;
+  int64_t t;
+  if (nunits % 8 == 0 && (nunits / 8) % a.nblk == 0) {
+    t = xcd_remap(blockIdx.x, nunits * NPART);
+    kpart = (int)(t % NPART);
+    t /= NPART;
+  } else {
+    t = gqa_unit(blockIdx.x, nunits, NPART, &kpart);
+  }
   const int64_t j = t % a.nblk; t /= a.nblk;
   const int hk = (int)(t % a.Hkv);
   const int64_t b = t / a.Hkv;
@@ -495,17 +528,21 @@ dkdv_kernel(BwdArgs a) {
   const int64_t seg = (b * a.hsel + hs) * a.nblk + j;
   const int e0 = a.seg_off[seg], e1 = a.seg_off[seg + 1];
 
-  const int u = kpart * C::NW * 16 + w * 16 + p;  // this lane's key row within block j (B-operand column)
+  const int role = ROLES == 2 ? (w & 1) : 0, kw = ROLES == 2 ? (w >> 1) : w;
+  const int u = kpart * KEYS + kw * 16 + p;  // this lane's key row within block j (B-operand column)
   const int64_t kpos = j * BS + u;
-  RowFrag<T, D> kf, vf;
-  kf.load((const T *)a.k + b * a.sk[0] + hk * a.sk[1] + kpos * a.sk[2], g);
-  vf.load((const T *)a.v + b * a.sv[0] + hk * a.sv[1] + kpos * a.sv[2], g);
+  const T *krow = (const T *)a.k + b * a.sk[0] + hk * a.sk[1] + kpos * a.sk[2];
+  const T *vrow = (const T *)a.v + b * a.sv[0] + hk * a.sv[1] + kpos * a.sv[2];
+  RowFrag<T, D> kf, vf;  // two roles: kf holds K (role 0) or V (role 1), vf is unused
+  kf.load(ROLES == 2 && role ? vrow : krow, g);
+  if constexpr (ROLES == 1) vf.load(vrow, g);
   const bool keyok = kpos < a.l_valid;
 
-  f32x4 dkacc[D / 16], dvacc[D / 16];
+  // two roles: dvacc accumulates dV (role 0) or dK (role 1)
+  f32x4 dkacc[ROLES == 2 ? 1 : D / 16], dvacc[D / 16];
 #pragma unroll
   for (int mt = 0; mt < D / 16; ++mt) {
-    dkacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROLES == 1) dkacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     dvacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
@@ -614,6 +651,40 @@ dkdv_kernel(BwdArgs a) {
         const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
         const float2 *Mh = Ms + h * HR;
         const int th = tmin - h * HR;
+        if constexpr (ROLES == 2) {
+          f32x4 xacc[HR / 16];
+          mm_rows_frag<T, D, HR / 16>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
+          float4 *xs = s_xch + (kw * 64 + lane) * (HR / 16);
+          float x[HR / 16][4];
+          if (role == 0) {
+#pragma unroll
+            for (int m = 0; m < HR / 16; ++m) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float2 ms = Mh[16 * m + 4 * g + r];
+                const bool ok = kok && (16 * m + r >= th);
+                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, gt - ms.x));
+                asm volatile("" : "+v"(ev));
+                x[m][r] = ok ? ev : 0.f;
+              }
+              xs[m] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
+            }
+          }
+          lds_barrier();  // P of this part is in LDS for the role-1 waves
+          if (role == 0) {
+            mm_tr_acc<T, D, HR>(Dh, x, dvacc, g, p);  // dV^T += dO^T P
+          } else {
+#pragma unroll
+            for (int m = 0; m < HR / 16; ++m) {
+              const float4 pv = xs[m];
+              const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
+            }
+            mm_tr_acc<T, D, HR>(Qh, x, dvacc, g, p);  // dK^T += Q^T dS
+          }
+          continue;
+        }
         f32x4 sacc[HR / 16], dpacc[HR / 16];
         mm_rows_frag<T, D, HR / 16>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
         mm_rows_frag<T, D, HR / 16>(Dh, vf, dpacc, g, p);  // dP
@@ -639,6 +710,18 @@ dkdv_kernel(BwdArgs a) {
     }
   }
 
+  if constexpr (ROLES == 2) {
+    T *row = (T *)(role ? a.dk : a.dv) + ((b * a.Hkv + hk) * a.L + kpos) * D;
+    const float sc = role ? a.scale : 1.f;
+#pragma unroll
+    for (int mt = 0; mt < D / 16; ++mt) {
+      s16x4 pk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)(dvacc[mt][r] * sc));
+      *(s16x4 *)(row + 16 * mt + 4 * g) = pk;
+    }
+    return;
+  }
   T *dkrow = (T *)a.dk + ((b * a.Hkv + hk) * a.L + kpos) * D;
   T *dvrow = (T *)a.dv + ((b * a.Hkv + hk) * a.L + kpos) * D;
 #pragma unroll
@@ -715,11 +798,13 @@ template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipS
 
 template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
   using C = DkdvCfg<T, BS, D>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16;
+  constexpr int HR = C::KC >= 64 ? 32 : C::KC;
+  const size_t xch = dkdv_roles<T, D>() == 2 ? (size_t)(dkdv_keys<T, BS, D>() / 16) * 64 * (HR / 16) * 16 : 0;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16 + xch;
   static size_t granted = 0;
   int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
   if (e) return e;
-  const int64_t nwg = a.B * a.Hkv * a.nblk * (BS / (C::NW * 16));
+  const int64_t nwg = a.B * a.Hkv * a.nblk * (BS / dkdv_keys<T, BS, D>());
   hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dkdv_kernel launch");
 }

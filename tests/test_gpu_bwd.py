@@ -78,7 +78,8 @@ def test_config2_output_gate():
     _cmp([got[4]], [ref[4]], "bf16", names=("dout_gate",))
 
 
-@pytest.mark.parametrize("bs,D", [(16, 64), (32, 32), (64, 128), (128, 64), (64, 256), (128, 256), (16, 32)])
+@pytest.mark.parametrize("bs,D", [(16, 64), (32, 32), (64, 128), (128, 64), (64, 256), (128, 256), (16, 32),
+                                  (16, 256), (32, 256)])
 def test_block_and_head_sizes_random_sel_with_duplicates(bs, D):
     # make_sel-style: own + random blocks with replacement (duplicates, future blocks), no mask
     g = torch.Generator().manual_seed(2)
