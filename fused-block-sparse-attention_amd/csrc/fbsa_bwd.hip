@@ -74,6 +74,32 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   lay->vals_out = off; off = al256(off + (size_t)lay->n * 4);
   lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
   lay->sort_tmp = off; off = al256(off + tmp);
+  // dK/dV list segments of at most ~4096 chunks per workgroup
+  const int64_t grp = d->Hq / d->Hkv;
+  const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
+  int64_t segE = 4096 / (grp * (d->bs / kc));
+  if (segE < 16) segE = 16;
+  lay->nwi = d->B * d->Hkv * d->nblk;
+  lay->seg_entries = d->nblk > segE ? segE : 0;
+  lay->xub = lay->slots_ub = 0;
+  lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
+  lay->scan_tmp_bytes = 0;
+  if (lay->seg_entries) {
+    const int64_t walked = lay->n * (d->Hkv / d->hsel);  // hsel is 1 or Hkv
+    lay->xub = walked / segE + 1;
+    lay->slots_ub = 2 * (walked / segE) + 1;
+    size_t stmp = 0;
+    e = hipcub::DeviceScan::ExclusiveSum(nullptr, stmp, (const uint64_t *)nullptr, (uint64_t *)nullptr,
+                                         (int)(lay->nwi + 1), (hipStream_t)0);
+    if (e != hipSuccess) return hip_check(e, "scan workspace query");
+    lay->scan_tmp_bytes = stmp;
+    lay->seg_cnt = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
+    lay->seg_pos = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
+    lay->wi_slot = off; off = al256(off + (size_t)lay->nwi * 4);
+    lay->xtab = off; off = al256(off + (size_t)lay->xub * 16);
+    lay->partials = off; off = al256(off + (size_t)lay->slots_ub * 2 * (size_t)(d->bs * d->D) * 4);
+    lay->scan_tmp = off; off = al256(off + stmp);
+  }
   lay->total = off;
   return FBSA_OK;
 }
@@ -257,6 +283,11 @@ struct BwdArgs {
   void *dq, *dk, *dv;
   float *dgate_part;
   const int32_t *seg_off, *ent;
+  const int32_t *wi_slot;  // list segments (null: none): first partial slot of a work item, or -1
+  const int4 *xtab;        // extra segments: (work item, first entry, end entry, partial slot)
+  const uint64_t *seg_tot; // extra segments << 32 | partial slots, in total
+  float *partials;         // [slot][dK, dV][bs rows][D] fp32
+  int64_t seg_entries, seg_entries_xub;  // segment length; bound on extra segments (grid size)
   int64_t B, Hq, Hkv, L, nblk, kk, hsel, l_valid;
   int64_t sq[3], sk[3], sv[3], sdo[3];
   float scale2, scale;
@@ -511,22 +542,41 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   // contiguous ranges. Otherwise (a share is part of a row) such ranges would
   // leave most of the work on a few XCDs: units go round-robin over the XCDs
   // instead. Either way a block's NPART workgroups run back to back on one XCD.
+  // A long list is walked in segments: the extra segments (all but a work
+  // item's first) come first in launch order, then one workgroup set per work
+  // item with its first segment (or whole list).
   const int64_t nunits = a.B * a.Hkv * a.nblk;
-  int kpart = 0;
+  const int64_t nx = a.wi_slot ? (int64_t)(*a.seg_tot >> 32) : 0;
+  int64_t bid = blockIdx.x;
+  int kpart = 0, slot = -1, e0 = 0, e1 = 0;
   int64_t t;
-  if (nunits % 8 == 0 && (nunits / 8) % a.nblk == 0) {
-    t = xcd_remap(blockIdx.x, nunits * NPART);
-    kpart = (int)(t % NPART);
-    t /= NPART;
+  const bool extra = bid < nx * NPART;
+  if (extra) {
+    const int4 xe = a.xtab[bid / NPART];
+    kpart = (int)(bid % NPART);
+    t = xe.x; e0 = xe.y; e1 = xe.z; slot = xe.w;
   } else {
-    t = gqa_unit(blockIdx.x, nunits, NPART, &kpart);
+    bid -= nx * NPART;
+    if (bid >= nunits * NPART) return;  // past the segments actually present
+    if (nunits % 8 == 0 && (nunits / 8) % a.nblk == 0) {
+      t = xcd_remap(bid, nunits * NPART);
+      kpart = (int)(t % NPART);
+      t /= NPART;
+    } else {
+      t = gqa_unit(bid, nunits, NPART, &kpart);
+    }
   }
+  const int64_t wi = t;
   const int64_t j = t % a.nblk; t /= a.nblk;
   const int hk = (int)(t % a.Hkv);
   const int64_t b = t / a.Hkv;
   const int hs = a.hsel == 1 ? 0 : hk;
   const int64_t seg = (b * a.hsel + hs) * a.nblk + j;
-  const int e0 = a.seg_off[seg], e1 = a.seg_off[seg + 1];
+  if (!extra) {
+    e0 = a.seg_off[seg];
+    e1 = a.seg_off[seg + 1];
+    if (a.wi_slot && (slot = a.wi_slot[wi]) >= 0) e1 = e0 + (int)a.seg_entries;
+  }
 
   const int role = ROLES == 2 ? (w & 1) : 0, kw = ROLES == 2 ? (w >> 1) : w;
   const int u = kpart * KEYS + kw * 16 + p;  // this lane's key row within block j (B-operand column)
@@ -710,6 +760,21 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
     }
   }
 
+  if (slot >= 0) {  // one segment of a split list: fp32 partials, summed by dkdv_reduce_kernel
+    float *pk = a.partials + ((int64_t)slot * 2 * BS + u) * D;  // dK rows, then dV rows
+    float *pv = pk + (int64_t)BS * D;
+#pragma unroll
+    for (int mt = 0; mt < D / 16; ++mt) {
+      const int d0 = 16 * mt + 4 * g;
+      if constexpr (ROLES == 2) {
+        *(f32x4 *)((role ? pk : pv) + d0) = dvacc[mt];
+      } else {
+        *(f32x4 *)(pk + d0) = dkacc[mt];
+        *(f32x4 *)(pv + d0) = dvacc[mt];
+      }
+    }
+    return;
+  }
   if constexpr (ROLES == 2) {
     T *row = (T *)(role ? a.dk : a.dv) + ((b * a.Hkv + hk) * a.L + kpos) * D;
     const float sc = role ? a.scale : 1.f;
@@ -744,6 +809,73 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   }
 }
 
+// List segments. Work item wi = (b, KV head, key block) walks the transposed
+// list of its selection head; longer than E entries it is cut into
+// S = ceil(len / E) segments. cnt[wi] = (S - 1) << 32 | S for a split item, 0
+// otherwise, and cnt[nwi] = 0, so that an exclusive scan gives each item's first
+// extra segment and first partial slot (high / low halves) and their totals.
+__global__ __launch_bounds__(256) void seg_count_kernel(const int32_t *seg_off, int64_t nwi, int64_t nblk, int64_t Hkv,
+                                                        int64_t hsel, int64_t E, uint64_t *cnt) {
+  const int64_t wi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (wi > nwi) return;
+  uint64_t c = 0;
+  if (wi < nwi) {
+    const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
+    const int64_t seg = (b * hsel + (hsel == 1 ? 0 : hk)) * nblk + j;
+    const int64_t len = seg_off[seg + 1] - seg_off[seg];
+    if (len > E) {
+      const uint64_t S = (uint64_t)((len + E - 1) / E);
+      c = ((S - 1) << 32) | S;
+    }
+  }
+  cnt[wi] = c;
+}
+
+// From the scanned counts: each work item's first partial slot (-1 when not
+// split) and the table rows of its extra segments 1 .. S-1.
+__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t *seg_off, const uint64_t *pos, int64_t nwi,
+                                                        int64_t nblk, int64_t Hkv, int64_t hsel, int64_t E,
+                                                        int32_t *wi_slot, int4 *xtab) {
+  const int64_t wi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (wi >= nwi) return;
+  const uint64_t p0 = pos[wi], p1 = pos[wi + 1];
+  const int ns = (int)((p1 - p0) & 0xffffffffu);
+  if (ns == 0) {
+    wi_slot[wi] = -1;
+    return;
+  }
+  const int slot0 = (int)(p0 & 0xffffffffu), x0 = (int)(p0 >> 32);
+  wi_slot[wi] = slot0;
+  const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
+  const int64_t seg = (b * hsel + (hsel == 1 ? 0 : hk)) * nblk + j;
+  const int e0 = seg_off[seg], e1 = seg_off[seg + 1];
+  for (int s = 1; s < ns; ++s) {
+    const int a0 = e0 + s * (int)E, a1 = e1 - a0 < (int)E ? e1 : a0 + (int)E;
+    xtab[x0 + s - 1] = int4{(int)wi, a0, a1, slot0 + s};
+  }
+}
+
+// dK, dV of a split work item: its S partials summed in segment order.
+template <typename T>
+__global__ __launch_bounds__(256) void dkdv_reduce_kernel(const int32_t *wi_slot, const uint64_t *pos,
+                                                          const float *partials, void *dk, void *dv, int64_t nblk,
+                                                          int64_t Hkv, int64_t L, int64_t bs, int64_t D, float scale) {
+  const int64_t wi = blockIdx.x;
+  const int slot0 = wi_slot[wi];
+  if (slot0 < 0) return;
+  const int ns = (int)((pos[wi + 1] - pos[wi]) & 0xffffffffu);
+  const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
+  const int64_t n = bs * D;
+  for (int64_t x = threadIdx.x; x < 2 * n; x += 256) {
+    const int which = x >= n;  // 0: dK, 1: dV
+    const int64_t e = x - which * n;
+    float acc = 0.f;
+    for (int s = 0; s < ns; ++s) acc += partials[((int64_t)(slot0 + s) * 2 + which) * n + e];
+    T *dst = (T *)(which ? dv : dk) + ((b * Hkv + hk) * L + j * bs) * D + e;
+    *dst = (T)(which ? acc : acc * scale);
+  }
+}
+
 // dgate[b, hs, i, s] = sum over the heads sharing selection hs (fixed order)
 __global__ __launch_bounds__(256) void dgate_reduce_kernel(const float *part, float *dgate, int64_t n, int64_t Hq,
                                                            int64_t hsel, int64_t nblk, int64_t kk, int64_t grp) {
@@ -757,6 +889,8 @@ __global__ __launch_bounds__(256) void dgate_reduce_kernel(const float *part, fl
 }
 
 static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, BwdArgs &a, const void *dout) {
+  a.wi_slot = nullptr; a.xtab = nullptr; a.seg_tot = nullptr; a.partials = nullptr;
+  a.seg_entries = a.seg_entries_xub = 0;
   a.B = d->B; a.Hq = d->Hq; a.Hkv = d->Hkv; a.L = d->L; a.nblk = d->nblk; a.kk = d->kk; a.hsel = d->hsel;
   a.l_valid = d->l_valid;
   for (int x = 0; x < 3; ++x) { a.sq[x] = d->sq[x]; a.sk[x] = d->sk[x]; a.sv[x] = d->sv[x]; a.sdo[x] = d->sdo[x]; }
@@ -804,7 +938,7 @@ template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hi
   static size_t granted = 0;
   int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
   if (e) return e;
-  const int64_t nwg = a.B * a.Hkv * a.nblk * (BS / dkdv_keys<T, BS, D>());
+  const int64_t nwg = (a.B * a.Hkv * a.nblk + (a.wi_slot ? a.seg_entries_xub : 0)) * (BS / dkdv_keys<T, BS, D>());
   hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dkdv_kernel launch");
 }
@@ -860,7 +994,47 @@ int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, c
   fill_bwd(d, lay, ws, a, dout);
   a.q = q; a.k = k; a.v = v; a.sel = nullptr; a.gate = gate; a.dq = nullptr; a.dk = dk; a.dv = dv;
   a.dgate_part = nullptr;
-  return bwd_dispatch(d, a, false, s);
+  int e;
+  if (lay.seg_entries) {
+    uint64_t *cnt = (uint64_t *)(ws + lay.seg_cnt), *pos = (uint64_t *)(ws + lay.seg_pos);
+    hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)((lay.nwi + 1 + 255) / 256)), dim3(256), 0, s,
+                       (const int32_t *)(ws + lay.seg_off), lay.nwi, d->nblk, d->Hkv, d->hsel, lay.seg_entries, cnt);
+    if ((e = hip_check(hipGetLastError(), "seg_count_kernel launch"))) return e;
+    size_t tmp = lay.scan_tmp_bytes;
+    if ((e = hip_check(hipcub::DeviceScan::ExclusiveSum(ws + lay.scan_tmp, tmp, (const uint64_t *)cnt, pos,
+                                                        (int)(lay.nwi + 1), s),
+                       "scan of the list segments")))
+      return e;
+    hipLaunchKernelGGL(seg_table_kernel, dim3((unsigned)((lay.nwi + 255) / 256)), dim3(256), 0, s,
+                       (const int32_t *)(ws + lay.seg_off), (const uint64_t *)pos, lay.nwi, d->nblk, d->Hkv, d->hsel,
+                       lay.seg_entries, (int32_t *)(ws + lay.wi_slot), (int4 *)(ws + lay.xtab));
+    if ((e = hip_check(hipGetLastError(), "seg_table_kernel launch"))) return e;
+    a.wi_slot = (const int32_t *)(ws + lay.wi_slot);
+    a.xtab = (const int4 *)(ws + lay.xtab);
+    a.seg_tot = pos + lay.nwi;
+    a.partials = (float *)(ws + lay.partials);
+    a.seg_entries = lay.seg_entries;
+    a.seg_entries_xub = lay.xub;
+  }
+  if ((e = bwd_dispatch(d, a, false, s)) || !lay.seg_entries) return e;
+  const dim3 g((unsigned)lay.nwi), blk(256);
+  const uint64_t *pos = (const uint64_t *)(ws + lay.seg_pos);
+  const float *part = (const float *)(ws + lay.partials);
+  const int32_t *wsl = (const int32_t *)(ws + lay.wi_slot);
+  switch (d->dtype) {
+    case FBSA_BF16:
+      hipLaunchKernelGGL(dkdv_reduce_kernel<bf16>, g, blk, 0, s, wsl, pos, part, dk, dv, d->nblk, d->Hkv, d->L, d->bs,
+                         d->D, d->scale);
+      break;
+    case FBSA_F16:
+      hipLaunchKernelGGL(dkdv_reduce_kernel<f16>, g, blk, 0, s, wsl, pos, part, dk, dv, d->nblk, d->Hkv, d->L, d->bs,
+                         d->D, d->scale);
+      break;
+    default:
+      hipLaunchKernelGGL(dkdv_reduce_kernel<float>, g, blk, 0, s, wsl, pos, part, dk, dv, d->nblk, d->Hkv, d->L, d->bs,
+                         d->D, d->scale);
+  }
+  return hip_check(hipGetLastError(), "dkdv_reduce_kernel launch");
 }
 
 }  // namespace fbsa

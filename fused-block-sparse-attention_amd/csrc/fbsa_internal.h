@@ -41,6 +41,12 @@ struct BwdLayout {
   int end_bit;     // radix-sort key bits
   size_t rowstat, dout_attn, dgate_part, keys_in, keys_out, vals_in, vals_out, seg_off, sort_tmp;
   size_t sort_tmp_bytes, total;
+  // dK/dV list segments: a (b, KV head, key block) whose list is longer than
+  // seg_entries (0: never) is walked by several workgroups that write fp32
+  // partials, summed in segment order by a second kernel
+  int64_t nwi;       // work items B * Hkv * nblk
+  int64_t seg_entries, xub, slots_ub;  // segment length, bounds on extra segments and partial slots
+  size_t seg_cnt, seg_pos, wi_slot, xtab, partials, scan_tmp, scan_tmp_bytes;
 };
 
 int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay);

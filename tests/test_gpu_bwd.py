@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import attn as oattn, select as osel
-from _util import randn, np64, assert_close
+from _util import randn, np64, assert_close, rel_l2, TOL, OUT_ROUND
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -108,6 +108,35 @@ def test_gqa_token_causal_padding_outgate(dtype, D):
     ref = _oracle(q, k, v, idx, do, "token_causal", l_valid=lv, out_gate=og, scale=0.0625)
     _cmp(got[:3], ref[:3], dtype)
     _cmp([got[4]], [ref[4]], dtype, names=("dout_gate",))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_long_lists_walked_in_segments(dtype):
+    # GQA 16:1, bs 16, d 256: one dK/dV workgroup walks at most 256 entries of a
+    # transposed list. Block 0 is selected twice in odd rows and once in even rows
+    # (576 entries: three segments whose fp32 partials are summed in order),
+    # block 1 once in even rows (192 entries: one workgroup)
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, N, D, bs, kk = 1, 16, 1, 6144, 256, 16, 4
+    nblk = N // bs
+    q, do = (randn(g, (B, Hq, N, D), dtype) for _ in range(2))
+    k, v = (randn(g, (B, Hkv, N, D), dtype) for _ in range(2))
+    i = torch.arange(nblk).view(1, nblk, 1)
+    rnd = torch.randint(2, nblk, (B, nblk, kk - 3), generator=g)
+    sel = torch.cat([i, torch.zeros_like(i), torch.where(i % 2 == 1, 0, 1), rnd], -1).numpy()[:, None]
+    got = _gpu_bwd(q, k, v, sel, do, "none")
+    ref = _oracle(q, k, v, sel, do, "none")
+    # a split list sums at least 4096 * 16 query rows per key, so block 0's dK/dV
+    # is large and carries the bf16 rounding of dS (rounded to the input dtype
+    # before its product, as in the reference kernel) in proportion: max-abs
+    # relative to the largest magnitude (as for dgate), relative L2 unscaled
+    t = TOL[dtype]
+    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
+        mag = max(1.0, float(np.max(np.abs(rv))))
+        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND[dtype] * np.abs(rv)))
+        rl = rel_l2(gv, rv)
+        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
+        assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
 
 
 def test_backward_is_bitwise_repeatable():
