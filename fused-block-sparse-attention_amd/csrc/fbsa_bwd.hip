@@ -16,11 +16,14 @@
 //                      P = exp2(S*scale*log2e + gate*log2e - lse*log2e),
 //                      dS = P (dP - delta), dQ^T += K^T dS^T; optional per-head
 //                      gate-gradient partials sum(dS) per slot.
-//   4. dkdv_kernel     one workgroup per (b, KV head, key block j), one wave
-//                      per 16 keys held in registers, walking j's transposed
-//                      list (times the GQA group's query heads): Q and dO
-//                      tiles of the reading query block through the ring,
-//                      S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+//   4. dkdv_kernel     one workgroup per (b, KV head, key block j) or part of
+//                      its keys, 16 keys per wave (or wave pair) held in
+//                      registers, walking j's transposed list (times the GQA
+//                      group's query heads): Q and dO tiles of the reading query
+//                      block through the ring, S = Q K^T, dP = dO V^T,
+//                      dV^T += dO^T P, dK^T += Q^T dS. A list longer than a
+//                      segment is walked by several workgroups writing fp32
+//                      partials, which dkdv_reduce_kernel sums in segment order.
 //
 // Reference semantics: src/triton_kernel.py:77-181 (recompute of P from the
 // same scores, the slot-0 triu / future-content masks, gate after scale,
