@@ -227,6 +227,27 @@ def qwen_main(a):
                      "kernel": "fbsa::fwd_kernel<bf16,128,256>", "flop_per_launch": flops},
         "cpu_baseline": None,
     }
+    if a.bwd:
+        # the backward of the same attention on the selector's indices (dO ~ N(0,1)):
+        # prep, transposed index, dQ and dK/dV, timed with HIP events on the stream
+        from fbsa_amd import ops
+        idx = S.select(q, k).to(torch.int32).contiguous()
+        do = torch.randn(B, Hq, N, D, generator=g, device=dev).to(torch.bfloat16)
+        sc = D ** -0.5
+        o, lse = ops.attention_forward(q, k, v, idx, mask=ops.MASK_TOKEN_CAUSAL, scale=sc, out_gate=og,
+                                       need_lse=True)
+        bwd_ev = []
+        for it in range(a.warmup + a.steps):
+            e0, e1 = ev(), ev()
+            e0.record(stream)
+            ops.attention_backward(q, k, v, idx, o, lse, do, mask=ops.MASK_TOKEN_CAUSAL, scale=sc, out_gate=og)
+            e1.record(stream)
+            if it >= a.warmup:
+                bwd_ev.append((e0, e1))
+        torch.cuda.synchronize()
+        t_bwd = sum(x.elapsed_time(y) for x, y in bwd_ev) / a.steps
+        out["ms_bwd"] = t_bwd
+        out["bwd_TFLOPs"] = 2.5 * flops / (t_bwd * 1e-3) / 1e12
     print(json.dumps(out), flush=True)
 
 
