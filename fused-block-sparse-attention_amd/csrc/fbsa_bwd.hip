@@ -115,6 +115,7 @@ struct PrepArgs {
   void *dout_attn, *dout_gate;
   int64_t Hq, L, rows;
   int64_t so[3], sdo[3], sog[3];
+  int og_vec;  // out-gate rows and dout_gate 16-byte aligned: vector loads and stores
 };
 
 template <typename T> __device__ __forceinline__ float half_to_f32(uint32_t h) {
@@ -162,14 +163,38 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(ov[e], dv[e], acc);
     if (a.og) {
+      float gv[8], dav[8], dgv[8];
       const T *grow = (const T *)a.og + b * a.sog[0] + h * a.sog[1] + t * a.sog[2] + 8 * c;
-      T *da = (T *)a.dout_attn + row * D + 8 * c;
-      T *dg = (T *)a.dout_gate + row * D + 8 * c;
+      if (a.og_vec) {
+        load8f<T>(grow, gv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gv[e] = (float)grow[e];
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float s = 1.f / (1.f + __expf(-(float)grow[e]));
-        da[e] = (T)(dv[e] * s);
-        dg[e] = (T)(dv[e] * ov[e] * (1.f - s));
+        const float s = 1.f / (1.f + __expf(-gv[e]));
+        dav[e] = dv[e] * s;
+        dgv[e] = dv[e] * ov[e] * (1.f - s);
+      }
+      T *da = (T *)a.dout_attn + row * D + 8 * c;
+      T *dg = (T *)a.dout_gate + row * D + 8 * c;
+      if constexpr (sizeof(T) == 4) {
+        *(f32x4 *)da = f32x4{dav[0], dav[1], dav[2], dav[3]};
+        *(f32x4 *)(da + 4) = f32x4{dav[4], dav[5], dav[6], dav[7]};
+      } else {
+        *(s16x8 *)da = pack8<T>(dav);  // workspace rows: 16-byte aligned
+      }
+      if (a.og_vec) {
+        if constexpr (sizeof(T) == 4) {
+          *(f32x4 *)dg = f32x4{dgv[0], dgv[1], dgv[2], dgv[3]};
+          *(f32x4 *)(dg + 4) = f32x4{dgv[4], dgv[5], dgv[6], dgv[7]};
+        } else {
+          *(s16x8 *)dg = pack8<T>(dgv);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dg[e] = (T)dgv[e];
       }
     }
   }
@@ -207,6 +232,9 @@ int run_bwd_prep(const fbsa_attn_desc *d, const BwdLayout &lay, const void *o, c
   a.dout_gate = dout_gate;
   a.Hq = d->Hq; a.L = d->L; a.rows = d->B * d->Hq * d->L;
   for (int x = 0; x < 3; ++x) { a.so[x] = d->so[x]; a.sdo[x] = d->sdo[x]; a.sog[x] = d->sog[x]; }
+  const int64_t es = esize(d->dtype);
+  a.og_vec = ((uintptr_t)out_gate % 16 == 0) && ((uintptr_t)dout_gate % 16 == 0) && (d->sog[0] * es) % 16 == 0 &&
+             (d->sog[1] * es) % 16 == 0 && (d->sog[2] * es) % 16 == 0;
   switch (d->dtype) {
     case FBSA_BF16: return prep_d<bf16>(a, d->D, s);
     case FBSA_F16: return prep_d<f16>(a, d->D, s);
