@@ -419,7 +419,7 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
     const int64_t row0 = (int64_t)s_blk[slot] * BS + ch * C::KC;
-    issue_tile_pair<T, C::KC, D, C::NW, C::LPT>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2], vbase,
+    issue_tile_pair<T, C::KC, D, C::NW, C::LPT, (D <= 64)>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2], vbase,
                                                 a.sv[2], row0, w, lane);
   };
 

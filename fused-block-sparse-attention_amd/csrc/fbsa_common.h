@@ -50,9 +50,10 @@ __host__ __device__ constexpr int swz(int row, int cpr) {
 // __syncthreads()); the "memory" clobber keeps LDS accesses from moving across
 // an issue. Waits the compiler inserts for its own loads stay correct (loads
 // leave vmcnt in issue order, so uncounted DMA only makes them wait longer).
-// M0 is written here without being preserved: these two are the only code in
-// the library that uses M0 (no LDS-DMA builtin, message, GWS or indexed
-// register move), so no value of the compiler's lives in it across the asm.
+// M0 is written here without being preserved. Apart from g2lds16_tracked below
+// (never used in a kernel that also uses these) nothing in the library uses M0
+// (no message, GWS or indexed register move), so no value of the compiler's
+// lives in it across the asm.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void g2lds16(const void *gsrc, void *lds_wave_base) {
@@ -64,6 +65,16 @@ __device__ __forceinline__ void g2lds4(const void *gsrc, void *lds_wave_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gsrc), "s"(m) : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// The same 16-byte copy through the compiler builtin: hipcc tracks it (and waits
+// vmcnt(0) before the next LDS read of the kernel). Measured faster than the
+// asm form for dq_kernel at d <= 64 (1.51 against 1.64 ms at 262144 tokens, four
+// workgroups per CU) and slower for every other ring kernel. The builtin keeps
+// M0 across consecutive copies, so a kernel uses this form or the asm one, never both.
+__device__ __forceinline__ void g2lds16_tracked(const void *gsrc, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
+                                   (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+}
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0] at bits 3:0, vmcnt[5:4] at bits 15:14, expcnt/lgkmcnt left open).

@@ -132,8 +132,9 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
 
 // Copy KC rows from each of two row-major sources into one LDS stage (two
 // swizzled tiles back to back) with direct-to-LDS 16-byte loads; every thread
-// issues LPT loads. Rows are src + (row0 + r) * stride.
-template <typename T, int KC, int D, int NW, int LPT>
+// issues LPT loads. Rows are src + (row0 + r) * stride. TRACKED: through the
+// compiler builtin (g2lds16_tracked) instead of the asm form.
+template <typename T, int KC, int D, int NW, int LPT, bool TRACKED = false>
 __device__ __forceinline__ void issue_tile_pair(char *st, const T *src0, int64_t stride0, const T *src1,
                                                 int64_t stride1, int64_t row0, int w, int lane) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
@@ -147,7 +148,8 @@ __device__ __forceinline__ void issue_tile_pair(char *st, const T *src0, int64_t
     const int row = rem / CPR, pos = rem % CPR;
     const int chunk = pos ^ swz(row, CPR);
     const T *src = part ? src1 + (row0 + row) * stride1 : src0 + (row0 + row) * stride0;
-    g2lds16(src + chunk * (16 / ES), st + wl * 1024);
+    if constexpr (TRACKED) g2lds16_tracked(src + chunk * (16 / ES), st + wl * 1024);
+    else g2lds16(src + chunk * (16 / ES), st + wl * 1024);
   }
 }
 
