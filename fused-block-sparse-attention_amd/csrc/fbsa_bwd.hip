@@ -896,14 +896,30 @@ __global__ __launch_bounds__(256) void dkdv_reduce_kernel(const int32_t *wi_slot
   if (slot0 < 0) return;
   const int ns = (int)((pos[wi + 1] - pos[wi]) & 0xffffffffu);
   const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
-  const int64_t n = bs * D;
-  for (int64_t x = threadIdx.x; x < 2 * n; x += 256) {
+  const int64_t n = bs * D;  // a multiple of 8: an 8-element group lies in dK or in dV
+  for (int64_t x = 8 * (int64_t)threadIdx.x; x < 2 * n; x += 8 * 256) {
     const int which = x >= n;  // 0: dK, 1: dV
     const int64_t e = x - which * n;
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) acc += partials[((int64_t)(slot0 + s) * 2 + which) * n + e];
-    T *dst = (T *)(which ? dv : dk) + ((b * Hkv + hk) * L + j * bs) * D + e;
-    *dst = (T)(which ? acc : acc * scale);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < ns; ++s) {
+      const float *src = partials + ((int64_t)(slot0 + s) * 2 + which) * n + e;
+      const f32x4 p0 = *(const f32x4 *)src, p1 = *(const f32x4 *)(src + 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[r] += p0[r];
+        acc[4 + r] += p1[r];
+      }
+    }
+    const float sc = which ? 1.f : scale;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] *= sc;
+    T *dst = (T *)(which ? dv : dk) + ((b * Hkv + hk) * L + j * bs) * D + e;  // 16-byte aligned
+    if constexpr (sizeof(T) == 4) {
+      *(f32x4 *)dst = f32x4{acc[0], acc[1], acc[2], acc[3]};
+      *(f32x4 *)(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    } else {
+      *(s16x8 *)dst = pack8<T>(acc);
+    }
   }
 }
 
