@@ -83,6 +83,8 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   int64_t segE = 4096 / (grp * (d->bs / kc));
   if (segE < 16) segE = 16;
   lay->nwi = d->B * d->Hkv * d->nblk;
+  if (lay->nwi >= 0x7fffffffLL)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: B * Hkv * nblk too large for the 32-bit list segments");
   lay->seg_entries = d->nblk > segE ? segE : 0;
   lay->xub = lay->slots_ub = 0;
   lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
