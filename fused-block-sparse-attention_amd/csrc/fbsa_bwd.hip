@@ -85,7 +85,10 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   lay->nwi = d->B * d->Hkv * d->nblk;
   if (lay->nwi >= 0x7fffffffLL)
     return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: B * Hkv * nblk too large for the 32-bit list segments");
-  lay->seg_entries = d->nblk > segE ? segE : 0;
+  // the longest possible list: token-causal selections are deduplicated, the
+  // other masks count a block chosen in several slots of a row once per slot
+  const int64_t maxlist = d->mask == FBSA_MASK_TOKEN_CAUSAL ? d->nblk : d->nblk * d->kk;
+  lay->seg_entries = maxlist > segE ? segE : 0;
   lay->xub = lay->slots_ub = 0;
   lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
   lay->scan_tmp_bytes = 0;

@@ -139,6 +139,29 @@ def test_long_lists_walked_in_segments(dtype):
         assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
 
 
+def test_duplicate_heavy_list_segments_half_blocks():
+    # bs 128, 16-bit d 256: each key block's dK/dV is split over two half-block
+    # workgroups (two waves per key group); every non-own slot of every row picks
+    # block 0 (mask none keeps duplicates), so its list has 5 * 33 + 1 = 166
+    # entries, more than one segment (128 at GQA 8, four chunks per block)
+    g = torch.Generator().manual_seed(6)
+    B, Hq, Hkv, N, D, bs, kk = 1, 8, 1, 640, 256, 128, 34
+    nblk = N // bs
+    q, do = (randn(g, (B, Hq, N, D), "bf16") for _ in range(2))
+    k, v = (randn(g, (B, Hkv, N, D), "bf16") for _ in range(2))
+    sel = np.zeros((B, 1, nblk, kk), np.int64)
+    sel[..., 0] = np.arange(nblk)
+    got = _gpu_bwd(q, k, v, sel, do, "none")
+    ref = _oracle(q, k, v, sel, do, "none")
+    t = TOL["bf16"]
+    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
+        mag = max(1.0, float(np.max(np.abs(rv))))  # block 0 sums 166 * 8 * 128 rows (see above)
+        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND["bf16"] * np.abs(rv)))
+        rl = rel_l2(gv, rv)
+        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
+        assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
+
+
 def test_backward_is_bitwise_repeatable():
     g = torch.Generator().manual_seed(4)
     B, H, N, D, bs, kk = 2, 4, 2048, 64, 64, 9
