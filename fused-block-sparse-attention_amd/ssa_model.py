@@ -463,4 +463,9 @@ class TinyTransformer(nn.Module):
                 if getattr(b["attn"], "last_block_logits", None) is not None]
 
     def centroid_align(self):
-        return []
+        """(align_q, align_k_all) of every layer that stashed them: the last
+        query block's centroid logits (B, C) and all key blocks' (B, nblk, C),
+        set by CentroidSSA when needle_pos is given (``src/ssa_model.py:560-562``);
+        train.py builds its centroid InfoNCE routing loss from these pairs."""
+        return [(b["attn"].align_q, b["attn"].align_k_all) for b in self.blocks
+                if getattr(b["attn"], "align_q", None) is not None]

@@ -255,6 +255,36 @@ def test_routed_modules_train_their_selectors():
     assert lsh.sel_q[0].weight.grad.abs().sum() > 0
 
 
+def test_tiny_transformer_centroid_align_trains_centroids():
+    # TinyTransformer.centroid_align (src/ssa_model.py:560-562) hands train.py
+    # (src/train.py:56-63) one (align_q, align_k_all) pair per CentroidSSA
+    # layer; the InfoNCE routing loss built from them reaches the centroids
+    from ssa_model import TinyTransformer
+    torch.manual_seed(3)
+    B, L, blk = 2, 512, 32
+    nblk = L // blk
+    m = TinyTransformer(64, 10, d=128, h=2, layers=2, max_len=L, attn="centroid",
+                        block=blk, sel_dim=16, n_centroids=4, cpq=2, cap=4).to(DEV)
+    toks = torch.randint(0, 64, (B, L), device=DEV)
+    npos = torch.tensor([37, 300], device=DEV)
+    assert m.centroid_align() == []                   # nothing stashed before a needle pass
+    m(toks, needle_pos=npos)
+    aligns = m.centroid_align()
+    assert len(aligns) == 2
+    tau, nb = 0.5, (npos // blk).long()
+    loss = 0.0
+    for aq, ak_all in aligns:
+        assert aq.shape == (B, 4) and ak_all.shape == (B, nblk, 4)
+        q_dist = F.softmax(aq.float() / tau, -1)
+        k_dist = F.softmax(ak_all.float() / tau, -1)
+        sim = (q_dist.unsqueeze(1) * k_dist).sum(-1) / tau
+        loss = loss + F.cross_entropy(sim, nb)
+    loss.backward()
+    for b in m.blocks:
+        g = b["attn"].cent.grad
+        assert g is not None and torch.isfinite(g).all() and g.abs().sum() > 0
+
+
 def test_blocksparse_gate_gradient_paths():
     # gather path (use_triton=False) trains the selector through the gate; the
     # fused op (use_triton=True) returns no gate gradient (src/triton_kernel.py:254)
