@@ -77,10 +77,12 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   lay->vals_out = off; off = al256(off + (size_t)lay->n * 4);
   lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
   lay->sort_tmp = off; off = al256(off + tmp);
-  // dK/dV list segments of at most ~4096 chunks per workgroup
+  // dK/dV list segments of at most ~4096 chunks per workgroup (512 for fp32
+  // operands: a segment's fp32 accumulator then sums 8x fewer rows, which keeps
+  // the rounding of sums over ~1e5 query rows under 1e-4 of the result's scale)
   const int64_t grp = d->Hq / d->Hkv;
   const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
-  int64_t segE = 4096 / (grp * (d->bs / kc));
+  int64_t segE = (d->dtype == FBSA_F32 ? 512 : 4096) / (grp * (d->bs / kc));
   if (segE < 16) segE = 16;
   lay->nwi = d->B * d->Hkv * d->nblk;
   if (lay->nwi >= 0x7fffffffLL)

@@ -62,7 +62,8 @@ def test_config2_gate_bias_and_dgate():
     dg, rdg = got[3], ref[3]
     rl = float(np.linalg.norm(dg - rdg) / np.linalg.norm(rdg))
     ma = float(np.max(np.abs(dg - rdg)) / max(1.0, np.max(np.abs(rdg))))
-    print(f"  dgate: max_abs/max|ref|={ma:.2e} rel_l2={rl:.2e}", flush=True)
+    print(f"  dgate: max_abs={float(np.max(np.abs(dg - rdg))):.2e} max|ref|={float(np.max(np.abs(rdg))):.1f} "
+          f"max_abs/max|ref|={ma:.2e} rel_l2={rl:.2e}", flush=True)
     assert rl <= 1e-2 and ma <= 2e-2
 
 
@@ -127,16 +128,18 @@ def test_long_lists_walked_in_segments(dtype):
     got = _gpu_bwd(q, k, v, sel, do, "none")
     ref = _oracle(q, k, v, sel, do, "none")
     # a split list sums at least 4096 * 16 query rows per key, so block 0's dK/dV
-    # is large and carries the bf16 rounding of dS (rounded to the input dtype
-    # before its product, as in the reference kernel) in proportion: max-abs
-    # relative to the largest magnitude (as for dgate), relative L2 unscaled
+    # is large; in 16-bit dtypes it carries the rounding of dS to the input dtype
+    # (before its product, as in the reference kernel) in proportion: max-abs
+    # relative to the largest magnitude (as for dgate), relative L2 unscaled.
+    # fp32 keeps the absolute 1e-4 bar.
     t = TOL[dtype]
     for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
         mag = max(1.0, float(np.max(np.abs(rv))))
         excess = float(np.max(np.abs(gv - rv) - OUT_ROUND[dtype] * np.abs(rv)))
         rl = rel_l2(gv, rv)
         print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
-        assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
+        bound = t["max_abs"] * (1.0 if dtype == "f32" else mag)
+        assert excess <= bound and rl <= t["rel_l2"], n
 
 
 def test_duplicate_heavy_list_segments_half_blocks():
