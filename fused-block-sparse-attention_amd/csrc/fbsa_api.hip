@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <math.h>
 
+#include <mutex>
+
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
 
@@ -153,9 +155,9 @@ int fbsa_select(const fbsa_select_desc *d, const void *a, const void *b1, const 
   return fbsa_select_rows(d, 0, d->nblk, a, b1, b2, sel, sel_score, workspace, workspace_bytes, stream);
 }
 
-int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a, const void *b1,
-                     const void *b2, int32_t *sel, float *sel_score, void *workspace, size_t workspace_bytes,
-                     void *stream) {
+// Argument checks of the selection entry points (no device work).
+static int check_select(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a,
+                        const void *b1, const void *b2, const int32_t *sel, const float *sel_score) {
   if (!d) return fail(FBSA_EINVAL, "fbsa_select: null descriptor");
   if (row_begin < 0 || row_end < row_begin || row_end > d->nblk)
     return fail(FBSA_EINVAL, "fbsa_select: row range [%lld, %lld) outside [0, %lld)", (long long)row_begin,
@@ -178,6 +180,14 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
     return fail(FBSA_EINVAL, "fbsa_select: misaligned pointer");
   const int64_t ntile = (d->nblk + 7) / 8;
   if (ntile * d->B * d->H > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_select: grid too large");
+  return FBSA_OK;
+}
+
+int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_end, const void *a, const void *b1,
+                     const void *b2, int32_t *sel, float *sel_score, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+  const int ce = check_select(d, row_begin, row_end, a, b1, b2, sel, sel_score);
+  if (ce) return ce;
   // Quest scores of wide operands (D >= 128, past the MFMA engine's widths)
   // under _finish for every row and without chosen-slot scores: the row-per-
   // workgroup exact kernel of fbsa_select_qmax with one query vector per block
@@ -342,6 +352,64 @@ int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
   if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);
   if (!e) e = fbsa_bwd_dkdv(d, q, k, v, dout, gate, dk, dv, workspace, workspace_bytes, stream);
   return e;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Selection without an allocation (fbsa_select_noalloc). The MFMA selection's
+// workspace (key norms and the per-chunk partial top-k lists) is taken from a
+// static device array instead of a caller's buffer. The array's name is a
+// host-side stand-in: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// handed to kernels. Every call on a device shares its array; the kernels
+// write every byte they later read (norms first, then the lists), so nothing
+// needs clearing between calls, and calls that overlap on one device race.
+namespace fbsa {
+
+static constexpr size_t kSelectScratchBytes = (size_t)FBSA_SELECT_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kSelectScratchBytes];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch array (looked up on first use).
+static int scratch_address(void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_check(e, "fbsa_select_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_select_noalloc: device ordinal %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_check(e, "fbsa_select_noalloc: hipGetSymbolAddress(scratch)");
+    if (!p || !aligned(p, 256)) return fail(FBSA_EHIP, "fbsa_select_noalloc: scratch address not 256-byte aligned");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FBSA_OK;
+}
+
+}  // namespace fbsa
+
+extern "C" {
+
+int fbsa_select_noalloc(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2, int32_t *sel,
+                        float *sel_score, void *stream) {
+  int e = check_select(d, 0, d ? d->nblk : 0, a, b1, b2, sel, sel_score);
+  if (e) return e;
+  const size_t need = select_workspace_bytes(d);
+  if (need > kSelectScratchBytes)
+    return fail(FBSA_EWORKSPACE,
+                "fbsa_select_noalloc: this selection needs %zu bytes of scratch, more than the %zu bytes of the "
+                "static scratch (call fbsa_select with a workspace instead)",
+                need, kSelectScratchBytes);
+  void *ws = nullptr;
+  if (need && (e = scratch_address(&ws))) return e;
+  return fbsa_select_rows(d, 0, d->nblk, a, b1, b2, sel, sel_score, ws, need, stream);
 }
 
 }  // extern "C"

@@ -19,6 +19,7 @@ SEL_OWN_FIRST, SEL_SORTED_SINK, SEL_SORTED_TOPK = 0, 1, 2
 QMAX_EXACT = 1
 SEL_CHUNK_SHIFT = 8
 FLAG_OUT_GATE = 1
+SELECT_SCRATCH_BYTES = 32 << 20   # FBSA_SELECT_SCRATCH_BYTES
 
 _i64x3 = ctypes.c_int64 * 3
 
@@ -85,6 +86,7 @@ SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "fbsa_select_rows": (ctypes.c_int, [ctypes.POINTER(SelectDesc), ctypes.c_int64, ctypes.c_int64,
                                         _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "fbsa_select_noalloc": (ctypes.c_int, [ctypes.POINTER(SelectDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "fbsa_select_qmax_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(QmaxDesc)]),
     "fbsa_select_qmax": (ctypes.c_int, [ctypes.POINTER(QmaxDesc), _vp, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_size_t, _vp]),

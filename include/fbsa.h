@@ -172,6 +172,21 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
                      const void *b1, const void *b2, int32_t *sel, float *sel_score, void *workspace,
                      size_t workspace_bytes, void *stream);
 
+/* fbsa_select without a workspace argument and without any allocation, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The MFMA selection's workspace comes from a static device array
+ * of FBSA_SELECT_SCRATCH_BYTES bytes that every GPU the library runs on holds
+ * until the process ends; the current device's array is used (the stream
+ * must belong to that device). A selection needing more
+ * (fbsa_select_workspace_bytes() > FBSA_SELECT_SCRATCH_BYTES) is rejected with
+ * FBSA_EWORKSPACE before any launch. All calls on one GPU share its array:
+ * calls that overlap on one GPU (two streams or threads) race. Results equal
+ * fbsa_select's. */
+#define FBSA_SELECT_SCRATCH_BYTES (32u << 20)
+int fbsa_select_noalloc(const fbsa_select_desc *d, const void *a, const void *b1, const void *b2,
+                        int32_t *sel, float *sel_score, void *stream);
+
 /* Row-block max Quest selection. The score of query block i and key block j
  * is the best Quest score over the tok query vectors of block i:
  *   score(i, j) = max_t rnd(rnd(relu(a_t).b1_j) + rnd(min(a_t,0).b2_j))
