@@ -3,15 +3,17 @@
 Workload (the north-star shape): bf16, B=1, H=8,
 D=64, N=262144, block 64 (nblk=4096), causal, top-16 content blocks by
 mean-pooled q.k scores (kk=17), q,k,v ~ N(0,1)/sqrt(D). One step = pool q,
-pool k, streaming top-k selection, fused forward (plus the backward when
---bwd is given), all on device-resident inputs, one after the other on one
+pool k, streaming top-k selection, fused forward, all on device-resident
+inputs, one after the other on one
 stream. ``--overlap`` times ``fbsa_amd.pipeline.select_and_attend`` instead,
 which overlaps the selection of later query blocks with the forward of
 earlier ones on a second stream (identical results; slower on MI355X at this
 shape, the two kernels contend for the CUs).
 
-Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step;
-``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
+Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step
+(BASELINE's headline); ``bwd`` times the backward of the same attention
+(prep, transposed index, dQ, dK/dV) with its own MFMA roofline (skip it with
+--no-bwd); ``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
 FLOP per launch, the reference's own formula, src/bench_crossover.py:105)
 timed with HIP events on the launch stream in separate, unoverlapped
 launches; ``cpu_baseline`` times the reference's PyTorch gather path on the
@@ -44,7 +46,9 @@ def parse():
     p.add_argument("--D", type=int, default=64)
     p.add_argument("--bs", type=int, default=64)
     p.add_argument("--topk", type=int, default=16)
-    p.add_argument("--bwd", action="store_true", help="also time the backward (separate fields)")
+    p.add_argument("--bwd", action="store_true", default=True,
+                   help="also time the backward (the default; its own fields and roofline)")
+    p.add_argument("--no-bwd", dest="bwd", action="store_false", help="skip the backward")
     p.add_argument("--graph", action="store_true",
                    help="time the step as one replayed HIP graph (fbsa_amd.pipeline.GraphStep)")
     p.add_argument("--overlap", action="store_true",
@@ -71,15 +75,39 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": 1 << 30, "launches": 3}), flush=True)
 
 
+KERNEL_SOURCES = {
+    # kernel -> the sources its code is built from (a traffic figure measured on
+    # other sources is stale and not reported)
+    "fwd_kernel": ["csrc/fbsa_fwd.hip", "csrc/fbsa_common.h", "csrc/fbsa_tiles.h"],
+    "dq_kernel": ["csrc/fbsa_bwd.hip", "csrc/fbsa_common.h", "csrc/fbsa_tiles.h"],
+    "dkdv_kernel": ["csrc/fbsa_bwd.hip", "csrc/fbsa_common.h", "csrc/fbsa_tiles.h"],
+}
+
+
+def source_sha(kernel):
+    """sha256 (16 hex digits) over the kernel's source files."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[kernel]:
+        with open(os.path.join(PKG, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profiles(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    copy-kernel calibrated) and recorded in profiles/traffic.json; None if absent."""
+    copy-kernel calibrated) and recorded in profiles/traffic.json together with
+    the sha of the kernel's sources and the commit it was measured at. Returns
+    (bytes, note): bytes is None when absent or measured on other sources."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)[workload][kernel]["bytes_per_launch"]
+            rec = json.load(f)[workload][kernel]
     except (OSError, KeyError, ValueError):
-        return None
+        return None, "not measured"
+    if rec.get("source_sha") != source_sha(kernel):
+        return None, f"stale: measured at {rec.get('commit', '?')} on other kernel sources"
+    return rec["bytes_per_launch"], f"rocprofv3 FETCH_SIZE+WRITE_SIZE at {rec.get('commit', '?')}, same sources"
 
 
 def cpu_baseline(q, k, v, bs, topk, rows_wanted):
@@ -97,6 +125,7 @@ def cpu_baseline(q, k, v, bs, topk, rows_wanted):
     import torch.nn.functional as F
 
     nthreads = torch.get_num_threads()
+    affinity = len(os.sched_getaffinity(0))
     qc, kc, vc = (t.detach().cpu() for t in (q, k, v))
     B, H, N, D = qc.shape
     nblk = N // bs
@@ -139,7 +168,9 @@ def cpu_baseline(q, k, v, bs, topk, rows_wanted):
     total = t_pool + (t_sel + t_fwd) * scale
     return {
         "value": B * N / total, "unit": "tokens/s", "cores": nthreads, "kind": "port",
-        "sample": (f"torch {str(qc.dtype).replace('torch.', '')} on {nthreads} host threads, the reference's "
+        "cpus_in_affinity_mask": affinity,
+        "sample": (f"torch {str(qc.dtype).replace('torch.', '')} on {nthreads} host threads (torch's intra-op "
+                   f"pool; {affinity} CPUs in the process affinity mask), the reference's "
                    f"gather path: full q/k pooling ({t_pool:.2f} s) + scores, top-k and gather attention for "
                    f"{len(rows)} of {nblk} query blocks x {H} heads ({t_sel + t_fwd:.2f} s), scaled "
                    f"x{scale:.1f} to all blocks; est. {total:.1f} s per step"),
@@ -337,6 +368,7 @@ def main():
     cfg_name = ("BASELINE configs[2]" if (N, shape) == (262144, (8, 64, 64, 16))
                 else "BASELINE configs[4] (selection-scaling stress)" if (N, shape) == (4194304, (8, 64, 64, 16))
                 else "custom shape")
+    traffic_b, traffic_note = traffic_from_profiles("fwd_kernel", wl)
     out = {
         "metric": (f"select+fwd tokens/s at {N // 1000}k tokens, 1 GPU (bf16, H{H} D{D} bs{bs} top-{topk}, causal)"),
         "value": B * N / (ms_step * 1e-3),
@@ -355,8 +387,8 @@ def main():
         "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS,
-                     "traffic": traffic_from_profiles("fwd_kernel", wl), "kernel": "fbsa::fwd_kernel<bf16,64,64>",
-                     "flop_per_launch": flops},
+                     "traffic": traffic_b, "traffic_source": traffic_note,
+                     "kernel": "fbsa::fwd_kernel<bf16,64,64>", "flop_per_launch": flops},
         "strict_roofline_select_fwd_us": None,
     }
     # strict roofline of the whole select+fwd step: selection reads q,k once (HBM), forward FLOPs (MFMA)
@@ -377,9 +409,19 @@ def main():
                 bwd_ev.append((e0, e1))
         torch.cuda.synchronize()
         t_bwd = sum(x.elapsed_time(y) for x, y in bwd_ev) / a.steps
+        # algorithmic backward work: 5 tile products per (query block, slot) against
+        # the forward's 2 (S, dP, dV, dQ, dK) = 2.5x the forward's FLOPs; this build
+        # recomputes S and dP in both the dQ and the dK/dV kernel (3.5x)
         bflops = 2.5 * flops
+        bach = bflops / (t_bwd * 1e-3) / 1e12
         out["ms_bwd"] = t_bwd
-        out["bwd_TFLOPs"] = bflops / (t_bwd * 1e-3) / 1e12
+        out["bwd"] = {"ms": t_bwd, "tokens_per_s": B * N / (t_bwd * 1e-3),
+                      "roofline": {"bound": "mfma", "achieved": bach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": bach / PEAK_BF16_TFLOPS, "flop_per_launch": bflops,
+                                   "implementation_flop_per_launch": 3.5 * flops,
+                                   "t_star_us": bflops / (PEAK_BF16_TFLOPS * 1e12) * 1e6},
+                      "stages": "prep (delta, lse), transposed index (stable radix sort), dQ, dK/dV"}
+        out["ms_select_fwd_bwd"] = ms_step + t_bwd
         out["train_step_tokens_per_s"] = B * N / ((ms_step + t_bwd) * 1e-3)
 
     if not a.no_cpu:
