@@ -60,6 +60,20 @@ static int check_attn(const fbsa_attn_desc *d, const char *fn) {
   return FBSA_OK;
 }
 
+// FBSA_FLAG_DENSE: the implicit all-blocks list (kk = nblk, no sel, no gate).
+static int check_dense(const fbsa_attn_desc *d, const void *sel, const void *gate, const char *fn) {
+  if (!(d->flags & FBSA_FLAG_DENSE)) {
+    if (!sel) return fail(FBSA_EINVAL, "%s: sel is NULL (only FBSA_FLAG_DENSE selects without a list)", fn);
+    return FBSA_OK;
+  }
+  if (d->kk != d->nblk) return fail(FBSA_EINVAL, "%s: FBSA_FLAG_DENSE needs kk == nblk (kk=%lld, nblk=%lld)", fn,
+                                    (long long)d->kk, (long long)d->nblk);
+  if (d->mask == FBSA_MASK_SLOT_CAUSAL)
+    return fail(FBSA_EINVAL, "%s: FBSA_FLAG_DENSE takes FBSA_MASK_TOKEN_CAUSAL or FBSA_MASK_NONE", fn);
+  if (gate) return fail(FBSA_EINVAL, "%s: FBSA_FLAG_DENSE takes no gate", fn);
+  return FBSA_OK;
+}
+
 static void fill_fwd(const fbsa_attn_desc *d, FwdArgs &a) {
   a.B = d->B; a.Hq = d->Hq; a.Hkv = d->Hkv; a.L = d->L; a.nblk = d->nblk; a.kk = d->kk; a.hsel = d->hsel;
   a.l_valid = d->l_valid;
@@ -69,6 +83,7 @@ static void fill_fwd(const fbsa_attn_desc *d, FwdArgs &a) {
   a.scale2 = d->scale * kLog2e;
   a.mask = d->mask;
   a.grp = (int)(d->Hq / d->Hkv);
+  a.dense = (d->flags & FBSA_FLAG_DENSE) ? 1 : 0;
 }
 
 }  // namespace fbsa
@@ -95,7 +110,9 @@ int fbsa_fwd_rows(const fbsa_attn_desc *d, int64_t i_begin, int64_t i_end, const
   if (i_begin < 0 || i_end < i_begin || i_end > d->nblk)
     return fail(FBSA_EINVAL, "fbsa_fwd: query-block range [%lld, %lld) outside [0, %lld)", (long long)i_begin,
                 (long long)i_end, (long long)d->nblk);
-  if (!q || !k || !v || !sel || !o) return fail(FBSA_EINVAL, "fbsa_fwd: null tensor pointer");
+  if (d->flags & ~FBSA_FLAG_DENSE) return fail(FBSA_EINVAL, "fbsa_fwd: unknown flags 0x%x", d->flags);
+  if ((e = check_dense(d, sel, gate, "fbsa_fwd"))) return e;
+  if (!q || !k || !v || !o) return fail(FBSA_EINVAL, "fbsa_fwd: null tensor pointer");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 16))
     return fail(FBSA_EINVAL, "fbsa_fwd: q/k/v/o must be 16-byte aligned");
   if (!aligned(sel, 4) || (gate && !aligned(gate, 4)) || (lse && !aligned(lse, 4)))
@@ -253,7 +270,8 @@ namespace fbsa {
 static int check_bwd(const fbsa_attn_desc *d, const char *fn, BwdLayout *lay, const void *ws, size_t ws_bytes) {
   int e = check_attn(d, fn);
   if (e) return e;
-  if (d->flags & ~FBSA_FLAG_OUT_GATE) return fail(FBSA_EINVAL, "%s: unknown flags 0x%x", fn, d->flags);
+  if (d->flags & ~(FBSA_FLAG_OUT_GATE | FBSA_FLAG_DENSE)) return fail(FBSA_EINVAL, "%s: unknown flags 0x%x", fn, d->flags);
+  if ((d->flags & FBSA_FLAG_DENSE) && (e = check_dense(d, nullptr, nullptr, fn))) return e;
   e = bwd_layout(d, lay);
   if (e) return e;
   if (!ws || !aligned(ws, 256)) return fail(FBSA_EINVAL, "%s: workspace must be non-null and 256-byte aligned", fn);
@@ -313,7 +331,8 @@ int fbsa_transpose_index(const fbsa_attn_desc *d, const int32_t *sel, void *work
   BwdLayout lay;
   int e = check_bwd(d, "fbsa_transpose_index", &lay, workspace, workspace_bytes);
   if (e) return e;
-  if (!sel || !aligned(sel, 4)) return fail(FBSA_EINVAL, "fbsa_transpose_index: sel must be non-null and 4-byte aligned");
+  if ((e = check_dense(d, sel, nullptr, "fbsa_transpose_index"))) return e;
+  if (sel && !aligned(sel, 4)) return fail(FBSA_EINVAL, "fbsa_transpose_index: sel must be 4-byte aligned");
   return run_transpose_index(d, lay, sel, (char *)workspace, (hipStream_t)stream);
 }
 
@@ -325,8 +344,10 @@ int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const voi
   if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dq");
   if (!e) e = check_dout(d, dout, "fbsa_bwd_dq");
   if (e) return e;
-  if (!sel || !aligned(sel, 4) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
-    return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned (sel non-null)");
+  if ((e = check_dense(d, sel, gate, "fbsa_bwd_dq"))) return e;
+  if ((d->flags & FBSA_FLAG_DENSE) && dgate) return fail(FBSA_EINVAL, "fbsa_bwd_dq: FBSA_FLAG_DENSE has no gate gradient");
+  if ((sel && !aligned(sel, 4)) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned");
   if (!dq || !aligned(dq, 16)) return fail(FBSA_EINVAL, "fbsa_bwd_dq: dq must be non-null and 16-byte aligned");
   return run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, (char *)workspace, (hipStream_t)stream);
 }
@@ -338,6 +359,7 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
   if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dkdv");
   if (!e) e = check_dout(d, dout, "fbsa_bwd_dkdv");
   if (e) return e;
+  if ((d->flags & FBSA_FLAG_DENSE) && gate) return fail(FBSA_EINVAL, "fbsa_bwd_dkdv: FBSA_FLAG_DENSE takes no gate");
   if (gate && !aligned(gate, 4)) return fail(FBSA_EINVAL, "fbsa_bwd_dkdv: gate must be 4-byte aligned");
   if (!dk || !dv || !aligned(dk, 16) || !aligned(dv, 16))
     return fail(FBSA_EINVAL, "fbsa_bwd_dkdv: dk/dv must be non-null and 16-byte aligned");

@@ -51,9 +51,46 @@ static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // ----------------------------------------------------------------- layout
+// Entries of key block j's transposed list under FBSA_FLAG_DENSE (every query
+// block i >= j when causal, every query block otherwise; none for a block past
+// l_valid), and the entries of the blocks before j.
+__host__ __device__ inline int64_t dense_count(int64_t j, int64_t nblk, int64_t nkb, bool causal) {
+  return j < nkb ? (causal ? nblk - j : nblk) : 0;
+}
+__host__ __device__ inline int64_t dense_prefix(int64_t j, int64_t nblk, int64_t nkb, bool causal) {
+  const int64_t m = j < nkb ? j : nkb;
+  return causal ? m * nblk - m * (m - 1) / 2 : m * nblk;
+}
+
 int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
-  lay->n = d->B * d->hsel * d->nblk * d->kk;
+  const bool dense = (d->flags & FBSA_FLAG_DENSE) != 0;
   lay->nseg = d->B * d->hsel * d->nblk;
+  if (dense) {
+    // the transposed lists are implicit: only their offsets are stored
+    const int64_t nkb = (d->l_valid + d->bs - 1) / d->bs;
+    const int64_t per = dense_prefix(d->nblk, d->nblk, nkb, d->mask == FBSA_MASK_TOKEN_CAUSAL);
+    if (lay->nseg >= 0x7fffffffLL || per >= (0x7fffffffLL / (d->B * d->hsel)))
+      return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: dense lists of %lld entries exceed the 32-bit transposed index",
+                  (long long)(per * d->B * d->hsel));
+    lay->n = 0;
+    lay->end_bit = 0;
+    lay->sort_tmp_bytes = 0;
+    const size_t rows = (size_t)(d->B * d->Hq * d->L);
+    size_t off = 0;
+    lay->rowstat = off; off = al256(off + rows * 8);
+    lay->dout_attn = off;
+    if (d->flags & FBSA_FLAG_OUT_GATE) off = al256(off + rows * (size_t)d->D * (size_t)esize(d->dtype));
+    lay->dgate_part = lay->keys_in = lay->keys_out = lay->vals_in = lay->vals_out = off;
+    lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
+    lay->sort_tmp = off;
+    lay->nwi = d->B * d->Hkv * d->nblk;
+    lay->seg_entries = lay->xub = lay->slots_ub = 0;  // lists are long for every block: no segments
+    lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
+    lay->scan_tmp_bytes = 0;
+    lay->total = off;
+    return FBSA_OK;
+  }
+  lay->n = d->B * d->hsel * d->nblk * d->kk;
   if (d->nblk * d->kk >= 0x7fffffffLL || lay->nseg >= 0x7fffffffLL || lay->n >= 0x7fffffffLL)
     return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: selection too large for the 32-bit transposed index");
   int bits = 1;
@@ -291,7 +328,23 @@ __global__ __launch_bounds__(256) void seg_off_kernel(const uint32_t *keys, int6
   seg_off[x] = (int32_t)lo;
 }
 
+// seg_off of the implicit dense lists: x = (b * hsel + hs) * nblk + j.
+__global__ __launch_bounds__(256) void dense_seg_off_kernel(int32_t *seg_off, int64_t nseg, int64_t nblk, int64_t nkb,
+                                                            int causal) {
+  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (x > nseg) return;
+  const int64_t grp = x / nblk, j = x % nblk;
+  seg_off[x] = (int32_t)(grp * dense_prefix(nblk, nblk, nkb, causal) + dense_prefix(j, nblk, nkb, causal));
+}
+
 int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int32_t *sel, char *ws, hipStream_t s) {
+  if (d->flags & FBSA_FLAG_DENSE) {
+    const int64_t nkb = (d->l_valid + d->bs - 1) / d->bs;
+    hipLaunchKernelGGL(dense_seg_off_kernel, dim3((unsigned)((lay.nseg + 1 + 255) / 256)), dim3(256), 0, s,
+                       (int32_t *)(ws + lay.seg_off), lay.nseg, d->nblk, nkb,
+                       d->mask == FBSA_MASK_TOKEN_CAUSAL ? 1 : 0);
+    return hip_check(hipGetLastError(), "dense_seg_off_kernel launch");
+  }
   IdxArgs a;
   a.sel = sel;
   a.keys = (uint32_t *)(ws + lay.keys_in);
@@ -330,6 +383,7 @@ struct BwdArgs {
   int64_t sq[3], sk[3], sv[3], sdo[3];
   float scale2, scale;
   int mask, grp;
+  int dense;  // FBSA_FLAG_DENSE: slot s is block s; lists implicit (i = j + position when causal)
 };
 
 // ROWS: the block rows one workgroup owns (one wave per 16), BS unless a
@@ -373,10 +427,11 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   const int hq = hk * a.grp + hin;
   const int hs = a.hsel == 1 ? 0 : hk;
 
-  // plan: compact list of valid slots (same rule as the forward)
+  // plan: compact list of valid slots (same rule as the forward; dense: implicit)
   const int64_t rowoff = ((b * a.hsel + hs) * a.nblk + i) * a.kk;
-  const int32_t *selrow = a.sel + rowoff;
-  if (w == 0) {
+  const int32_t *selrow = a.dense ? nullptr : a.sel + rowoff;
+  const int nkb = (int)((a.l_valid + BS - 1) / BS);  // key blocks holding a valid key
+  if (!a.dense && w == 0) {
     int nout = 0;
     for (int s0 = 0; s0 < a.kk; s0 += 64) {
       const int s = s0 + lane;
@@ -418,14 +473,22 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   const float2 rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
   const float lse2 = rs.x, delta = rs.y;
   __syncthreads();
-  const int nv = s_nvalid;
+  const int nv = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
+  auto blk_of = [&](int slot) { return a.dense ? slot : s_blk[slot]; };
+  auto kind_of = [&](int slot) {
+    if (!a.dense) return s_kind[slot];
+    const int64_t jj = slot;
+    const bool pad = (jj + 1) * BS > a.l_valid;
+    return a.mask == FBSA_MASK_TOKEN_CAUSAL ? ((jj == i || pad) ? (int)KIND_ABS : (int)KIND_FULL)
+                                            : (pad ? (int)KIND_PAD : (int)KIND_FULL);
+  };
 
   const T *kbase = (const T *)a.k + b * a.sk[0] + hk * a.sk[1];
   const T *vbase = (const T *)a.v + b * a.sv[0] + hk * a.sv[1];
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int64_t row0 = (int64_t)s_blk[slot] * BS + ch * C::KC;
+    const int64_t row0 = (int64_t)blk_of(slot) * BS + ch * C::KC;
     issue_tile_pair<T, C::KC, D, C::NW, C::LPT, (D <= 64)>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2], vbase,
                                                 a.sv[2], row0, w, lane);
   };
@@ -456,9 +519,9 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
     const char *Vs = Ks + C::TILE_BYTES;
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int kind = s_kind[slot];
-    const float gt = s_gate[slot];
-    const int64_t j = s_blk[slot];
+    const int kind = kind_of(slot);
+    const float gt = a.dense ? 0.f : s_gate[slot];
+    const int64_t j = blk_of(slot);
 
     f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
     mm_rows_frag<T, D, C::KC / 16>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
@@ -650,12 +713,22 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
     tdo[n] = part != 0;
   }
 
+  // dense lists: entry at position e of block j's list is query block dense_i0 + e
+  const int64_t dense_i0 = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL ? j : 0) - a.seg_off[seg] : 0;
   for (int eb = e0; eb < e1; eb += MAXE) {
     const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
     __syncthreads();  // the previous batch's entries are no longer read
     for (int x = tid; x < ne; x += C::NT) {
-      const int ev = a.ent[eb + x];
-      const int i = (int)(ev / a.kk), s = (int)(ev % a.kk);
+      // dense: the list of block j is query blocks j.. (causal) or 0.., slot j
+      int i, s;
+      if (a.dense) {
+        i = (int)(dense_i0 + eb + x);
+        s = (int)j;
+      } else {
+        const int ev = a.ent[eb + x];
+        i = (int)(ev / a.kk);
+        s = (int)(ev % a.kk);
+      }
       int kind = KIND_FULL;
       if (a.mask == FBSA_MASK_SLOT_CAUSAL) kind = s == 0 ? KIND_DIAG : KIND_FULL;
       else if (a.mask == FBSA_MASK_NONE) kind = (j + 1) * BS > a.l_valid ? KIND_PAD : KIND_FULL;
@@ -961,6 +1034,8 @@ static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, Bw
   a.scale2 = d->scale * kLog2e;
   a.mask = d->mask;
   a.grp = (int)(d->Hq / d->Hkv);
+  a.dense = (d->flags & FBSA_FLAG_DENSE) ? 1 : 0;
+  if (a.dense) a.ent = nullptr;
 }
 
 template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, const char *what) {
@@ -976,7 +1051,7 @@ template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, co
 
 template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipStream_t s) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (a.dense ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
   static size_t granted = 0;
   int e = set_lds(dq_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dq");
   if (e) return e;

@@ -87,9 +87,12 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   const int hs = a.hsel == 1 ? 0 : hk;
 
   // ---- 1. plan: compact list of valid slots with their mask kind and gate ----
+  // (dense: slot s is block s for the blocks below l_valid, and up to i when
+  // causal; kinds follow from the block index, no table)
   const int64_t rowoff = ((b * a.hsel + hs) * a.nblk + i) * a.kk;
-  const int32_t *selrow = a.sel + rowoff;
-  if (w == 0) {
+  const int32_t *selrow = a.dense ? nullptr : a.sel + rowoff;
+  const int nkb = (int)((a.l_valid + BS - 1) / BS);  // key blocks holding a valid key
+  if (!a.dense && w == 0) {
     int nout = 0;
     for (int s0 = 0; s0 < a.kk; s0 += 64) {
       const int s = s0 + lane;
@@ -157,15 +160,23 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     doff[n] = (int32_t)(((int64_t)row * (part ? a.sv[2] : a.sk[2]) + chunk * (16 / C::ES)) * C::ES);
   }
   __syncthreads();
-  const int nv = s_nvalid;
+  const int nv = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
+  auto blk_of = [&](int slot) { return a.dense ? slot : s_blk[slot]; };
+  auto kind_of = [&](int slot) {
+    if (!a.dense) return s_kind[slot];
+    const int64_t jj = slot;
+    const bool pad = (jj + 1) * BS > a.l_valid;
+    return a.mask == FBSA_MASK_TOKEN_CAUSAL ? ((jj == i || pad) ? (int)KIND_ABS : (int)KIND_FULL)
+                                            : (pad ? (int)KIND_PAD : (int)KIND_FULL);
+  };
 
   const char *kbase = (const char *)((const T *)a.k + b * a.sk[0] + hk * a.sk[1]);
   const char *vbase = (const char *)((const T *)a.v + b * a.sv[0] + hk * a.sv[1]);
   const int64_t kstep = a.sk[2] * C::ES, vstep = a.sv[2] * C::ES;
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(s_blk[slot] * BS + ch * C::KC);
+    const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(blk_of(slot) * BS + ch * C::KC);
     const char *kb = kbase + row0 * kstep, *vb = vbase + row0 * vstep;
     char *st = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
 #pragma unroll
@@ -213,9 +224,9 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
     const char *Vs = Ks + C::TILE_BYTES;
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int kind = s_kind[slot];
-    const float gt = s_gate[slot];
-    const int64_t j = s_blk[slot];
+    const int kind = kind_of(slot);
+    const float gt = a.dense ? 0.f : s_gate[slot];
+    const int64_t j = blk_of(slot);
 
     // V^T fragments for the PV product, shared by the query tiles; issued first
     // so their LDS latency overlaps the score MFMAs and the softmax
@@ -424,7 +435,7 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
 template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
 static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
   using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (size_t)a.kk * 12;
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (a.dense ? 0 : (size_t)a.kk * 12);
   if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: kk=%lld needs %zu bytes of LDS", (long long)a.kk, lds);
   if (lds > 64 * 1024) {
     static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation

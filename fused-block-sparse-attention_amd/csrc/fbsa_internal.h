@@ -21,6 +21,7 @@ struct FwdArgs {
   float scale2;  // softmax scale * log2(e)
   int mask;
   int grp;
+  int dense;     // FBSA_FLAG_DENSE: slot s is block s, sel and gate unused
 };
 
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);

@@ -18,7 +18,7 @@ SCORE_DOT, SCORE_MAX2, SCORE_QUEST = 0, 1, 2
 SEL_OWN_FIRST, SEL_SORTED_SINK, SEL_SORTED_TOPK = 0, 1, 2
 QMAX_EXACT = 1
 SEL_CHUNK_SHIFT = 8
-FLAG_OUT_GATE = 1
+FLAG_OUT_GATE, FLAG_DENSE = 1, 2
 SELECT_SCRATCH_BYTES = 32 << 20   # FBSA_SELECT_SCRATCH_BYTES
 
 _i64x3 = ctypes.c_int64 * 3

@@ -21,13 +21,16 @@ class BlockSparseAttention(torch.autograd.Function):
     def forward(ctx, q, k, v, sel, gate, out_gate, mask, scale, l_valid, gate_grad):
         o, lse = ops.attention_forward(q, k, v, sel, mask=mask, scale=scale, gate=gate, l_valid=l_valid,
                                        out_gate=out_gate, need_lse=True)
-        ctx.save_for_backward(q, k, v, sel, gate, out_gate, o, lse)
+        ctx.dense = sel if isinstance(sel, ops.DenseSelection) else None
+        ctx.save_for_backward(q, k, v, None if ctx.dense is not None else sel, gate, out_gate, o, lse)
         ctx.mask, ctx.scale, ctx.l_valid, ctx.gate_grad = mask, scale, l_valid, gate_grad
         return o
 
     @staticmethod
     def backward(ctx, do):
         q, k, v, sel, gate, out_gate, o, lse = ctx.saved_tensors
+        if ctx.dense is not None:
+            sel = ctx.dense
         need_dg = gate is not None and ctx.gate_grad and ctx.needs_input_grad[4]
         dq, dk, dv, dgate, dog = ops.attention_backward(
             q, k, v, sel, o, lse, do, mask=ctx.mask, scale=ctx.scale, gate=gate, l_valid=ctx.l_valid,
@@ -39,7 +42,8 @@ class BlockSparseAttention(torch.autograd.Function):
 
 def block_sparse_attention(q, k, v, sel, *, mask, scale=None, gate=None, out_gate=None, l_valid=None,
                            gate_grad=True):
-    """Differentiable fused block-sparse attention; sel is (B, Hsel, nblk, kk)."""
+    """Differentiable fused block-sparse attention; sel is (B, Hsel, nblk, kk)
+    or an ``ops.DenseSelection`` (every block)."""
     return BlockSparseAttention.apply(q, k, v, sel, gate, out_gate, mask, scale, l_valid, gate_grad)
 
 

@@ -14,6 +14,19 @@ SUPPORTED_BS = (16, 32, 64, 128)
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
 
+class DenseSelection:
+    """Every key block selected, slot s holding block s (FBSA_FLAG_DENSE): the
+    implicit (B, 1, nblk, nblk) list of dense attention, never stored. With
+    MASK_TOKEN_CAUSAL query block i reads blocks 0..i, with MASK_NONE all; the
+    dense fast path of ``blocksparse_forward`` (src/qwen_blocksparse.py:37-41)."""
+
+    def __init__(self, B, nblk):
+        self.shape = (B, 1, nblk, nblk)
+
+    def dim(self):
+        return 4
+
+
 def _dtype_code(t):
     try:
         return _DT[t.dtype]
@@ -72,7 +85,7 @@ def make_desc(q, k, v, o, sel, *, mask, scale, l_valid, dout=None, out_gate=None
     d.nblk, d.kk, d.hsel = nblk, kk, hsel
     d.l_valid = L if l_valid is None else int(l_valid)
     d.scale = float(scale)
-    d.flags = 0
+    d.flags = _lib.FLAG_DENSE if isinstance(sel, DenseSelection) else 0
     d.sq[:] = _strides3(q)
     d.sk[:] = _strides3(k)
     d.sv[:] = _strides3(v)
@@ -83,6 +96,10 @@ def make_desc(q, k, v, o, sel, *, mask, scale, l_valid, dout=None, out_gate=None
 
 
 def _check_common(q, k, v, sel, gate):
+    if isinstance(sel, DenseSelection):
+        if gate is not None:
+            raise ValueError("fbsa: a dense selection takes no gate")
+        sel = None
     _require_cuda(q, k, v, sel, gate)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("fbsa: q, k, v must be 4-D (B, H, L, D)")
@@ -90,7 +107,7 @@ def _check_common(q, k, v, sel, gate):
         raise ValueError(f"fbsa: shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError("fbsa: q, k, v must share a dtype")
-    if sel.dim() != 4 or sel.shape[0] != q.shape[0]:
+    if sel is not None and (sel.dim() != 4 or sel.shape[0] != q.shape[0]):
         raise ValueError(f"fbsa: sel must be (B, Hsel, nblk, kk), got {tuple(sel.shape)}")
     if gate is not None and gate.shape != sel.shape:
         raise ValueError(f"fbsa: gate shape {tuple(gate.shape)} != sel shape {tuple(sel.shape)}")
@@ -113,15 +130,16 @@ def prepare_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None, 
         og = _pad_d(out_gate, Dp)
         if og.stride(-1) != 1:
             og = og.contiguous()
-    sel32 = sel.to(torch.int32).contiguous()
+    dense = isinstance(sel, DenseSelection)
+    sel32 = sel if dense else sel.to(torch.int32).contiguous()
     gate32 = gate.to(torch.float32).contiguous() if gate is not None else None
     o = torch.empty(B, Hq, L, Dp, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, Hq, L, dtype=torch.float32, device=q.device) if need_lse else None
     if sel32.shape[2] == 0 or L % sel32.shape[2]:
         raise ValueError(f"fbsa: L={L} is not a multiple of nblk={sel32.shape[2]}")
     d = make_desc(qk[0], qk[1], qk[2], o, sel32, mask=mask, scale=scale, l_valid=l_valid, out_gate=og)
-    return {"d": d, "qkv": qk, "sel": sel32, "gate": gate32, "og": og, "o": o, "lse": lse, "D": D, "Dp": Dp,
-            "nblk": sel32.shape[2]}
+    return {"d": d, "qkv": qk, "sel": None if dense else sel32, "gate": gate32, "og": og, "o": o, "lse": lse,
+            "D": D, "Dp": Dp, "nblk": sel32.shape[2]}
 
 
 def launch_forward(prep, blocks=None):
@@ -146,7 +164,7 @@ def attention_forward(q, k, v, sel, *, mask, scale=None, gate=None, l_valid=None
     """Fused block-sparse attention forward.
 
     q (B,Hq,L,D); k, v (B,Hkv,L,D); sel (B,Hsel,nblk,kk) integer block ids with
-    Hsel in {1, Hkv}; gate (B,Hsel,nblk,kk) additive bias (cast to fp32);
+    Hsel in {1, Hkv}, or a ``DenseSelection`` (every block, no list); gate (B,Hsel,nblk,kk) additive bias (cast to fp32);
     out_gate (B,Hq,L,D) (any strides): o <- o * sigmoid(out_gate).
     Returns o (and the fp32 natural-log LSE (B,Hq,L) when need_lse).
     """
@@ -185,7 +203,8 @@ def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=Non
         og = _pad_d(out_gate, Dp)
         if og.stride(-1) != 1:
             og = og.contiguous()
-    sel32 = sel.to(torch.int32).contiguous()
+    dense = isinstance(sel, DenseSelection)
+    sel32 = sel if dense else sel.to(torch.int32).contiguous()
     gate32 = gate.to(torch.float32).contiguous() if gate is not None else None
     lse_c = lse.contiguous()
     nblk = sel32.shape[2]
@@ -199,7 +218,7 @@ def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=Non
     dog = torch.empty(B, Hq, L, Dp, dtype=q.dtype, device=dev) if og is not None else None
     d = make_desc(qk[0], qk[1], qk[2], o_p, sel32, mask=mask, scale=scale, l_valid=l_valid, dout=do_p,
                   out_gate=og)
-    d.flags = _lib.FLAG_OUT_GATE if og is not None else 0
+    d.flags |= _lib.FLAG_OUT_GATE if og is not None else 0
     lib = _lib.load()
     nbytes = lib.fbsa_bwd_workspace_bytes(d)
     if nbytes == 0:
@@ -208,7 +227,7 @@ def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=Non
     base = ws.data_ptr()
     wp = (base + 255) // 256 * 256
     _lib.check(lib.fbsa_bwd(d, _ptr(qk[0]), _ptr(qk[1]), _ptr(qk[2]), _ptr(o_p), _ptr(do_p), _ptr(lse_c),
-                            _ptr(sel32), _ptr(gate32), _ptr(og), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dgate),
+                            None if dense else _ptr(sel32), _ptr(gate32), _ptr(og), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dgate),
                             _ptr(dog), wp, nbytes, _stream()), "fbsa_bwd")
     if Dp != D:
         dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]

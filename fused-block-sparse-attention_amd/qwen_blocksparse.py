@@ -55,19 +55,21 @@ def blocksparse_forward(q, k, v, *, selector, topk, bs, causal=True, scale=None,
     scale = d ** -0.5 if scale is None else scale
     nblk = (L + bs - 1) // bs
     if selector is None and topk >= nblk:
-        idx = torch.arange(nblk, device=q.device, dtype=torch.int32).view(1, 1, 1, nblk).expand(B, Hkv, nblk, nblk)
+        # dense fast path: every block, causal or full, with no block list
+        # (the kernels enumerate the blocks themselves; any length)
+        sel = ops.DenseSelection(B, nblk)
         mask = ops.MASK_TOKEN_CAUSAL if causal else ops.MASK_NONE
     else:
         idx = selector.select(q, k)
         mask = ops.MASK_TOKEN_CAUSAL
-    if tuple(idx.shape[:3]) != (B, Hkv, nblk):
-        raise ValueError(f"selector returned {tuple(idx.shape)}, expected ({B}, {Hkv}, {nblk}, kk)")
+        if tuple(idx.shape[:3]) != (B, Hkv, nblk):
+            raise ValueError(f"selector returned {tuple(idx.shape)}, expected ({B}, {Hkv}, {nblk}, kk)")
+        sel = idx.to(torch.int32).contiguous()
     qp, _, pad = _pad_blocks(q, bs)
     kp, _, _ = _pad_blocks(k, bs)
     vp, _, _ = _pad_blocks(v, bs)
     og = _pad_blocks(out_gate, bs)[0] if out_gate is not None else None
-    out = block_sparse_attention(qp, kp, vp, idx.to(torch.int32).contiguous(), mask=mask, scale=scale,
-                                 out_gate=og, l_valid=L)
+    out = block_sparse_attention(qp, kp, vp, sel, mask=mask, scale=scale, out_gate=og, l_valid=L)
     return out[..., :L, :] if pad else out
 
 

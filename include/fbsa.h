@@ -59,7 +59,7 @@ typedef struct fbsa_attn_desc {
   int64_t hsel;    /* 1 or Hkv */
   int64_t l_valid; /* positions >= l_valid are padding keys (NONE, TOKEN_CAUSAL) */
   float scale;     /* softmax scale applied to q.k before the gate bias */
-  int32_t flags;   /* FBSA_FLAG_* bits (backward only; 0 for the forward) */
+  int32_t flags;   /* FBSA_FLAG_* bits (DENSE: forward and backward; OUT_GATE: backward only) */
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sog[3];
 } fbsa_attn_desc;
 
@@ -224,8 +224,17 @@ int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, con
 
 /* fbsa_attn_desc.flags bits. OUT_GATE: the backward will be given out_gate
  * (the forward applied o <- o * sigmoid(out_gate)); the workspace then also
- * holds the gate-scaled upstream gradient. */
-enum { FBSA_FLAG_OUT_GATE = 1 };
+ * holds the gate-scaled upstream gradient.
+ * DENSE (forward and backward): every key block is selected, slot s holding
+ * block s (kk must equal nblk); sel is not read (may be NULL) and gate must be
+ * NULL. With FBSA_MASK_TOKEN_CAUSAL query block i reads blocks 0..i (causal
+ * dense attention), with FBSA_MASK_NONE every block; keys at or past l_valid
+ * are padding in both. The block list is implicit, so the forward takes any
+ * length, and the backward's transposed lists need no sort (their total,
+ * B * hsel * the number of (query block, key block) pairs, must stay below
+ * 2^31). Replaces the SDPA fast path of blocksparse_forward
+ * (src/qwen_blocksparse.py:37-41). */
+enum { FBSA_FLAG_OUT_GATE = 1, FBSA_FLAG_DENSE = 2 };
 
 /* Workspace for the backward stages below (one opaque region, 256-byte
  * aligned): per-row softmax statistics, the block-transposed index (CSR of

@@ -145,3 +145,34 @@ def test_python_ops_require_gpu_tensors():
     sel = torch.zeros(1, 1, 1, 1, dtype=torch.int32)
     with pytest.raises(ValueError, match="GPU"):
         ops.attention_forward(q, q, q, sel, mask=ops.MASK_SLOT_CAUSAL)
+
+
+def test_dense_flag_validation_and_small_backward_workspace():
+    # FBSA_FLAG_DENSE: implicit all-blocks list (kk == nblk, no sel, no gate,
+    # token-causal or none); its backward stores only the list offsets
+    lib = _lib.load()
+    d = _desc(kk=4, mask=_lib.MASK_TOKEN_CAUSAL)
+    d.flags = _lib.FLAG_DENSE
+    d.kk = 3
+    assert lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, None, None, None, DUMMY, None, None) == _lib.EINVAL
+    assert "kk == nblk" in lib.fbsa_last_error().decode()
+    d.kk, d.mask = 4, _lib.MASK_SLOT_CAUSAL
+    assert lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, None, None, None, DUMMY, None, None) == _lib.EINVAL
+    assert "TOKEN_CAUSAL" in lib.fbsa_last_error().decode()
+    d.mask = _lib.MASK_TOKEN_CAUSAL
+    assert lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, None, DUMMY, None, DUMMY, None, None) == _lib.EINVAL
+    assert "gate" in lib.fbsa_last_error().decode()
+    d.flags = 0   # a list-less call needs the dense flag
+    assert lib.fbsa_fwd(d, DUMMY, DUMMY, DUMMY, None, None, None, DUMMY, None, None) == _lib.EINVAL
+    assert "sel is NULL" in lib.fbsa_last_error().decode()
+    # 1M tokens at block 64 (16384 blocks), 8 heads: the dense backward's workspace is
+    # the row statistics plus the list offsets, no per-entry arrays
+    big = _desc(mask=_lib.MASK_TOKEN_CAUSAL, Hq=8, Hkv=8, L=16384 * 64, nblk=16384, kk=16384, l_valid=16384 * 64)
+    for s in ("sq", "sk", "sv", "so", "sdo", "sog"):
+        getattr(big, s)[:] = (8 * 16384 * 64 * 64, 16384 * 64 * 64, 64)
+    big.flags = _lib.FLAG_DENSE
+    rows = 8 * 16384 * 64
+    nbytes = lib.fbsa_bwd_workspace_bytes(big)
+    assert rows * 8 <= nbytes <= rows * 8 + (16384 + 1) * 4 + 1024
+    big.flags = 0   # the same shape as an explicit list would need nblk^2 sort entries: refused
+    assert lib.fbsa_bwd_workspace_bytes(big) == 0
