@@ -190,7 +190,9 @@ static int check_select(const fbsa_select_desc *d, int64_t row_begin, int64_t ro
   if (d->convention == FBSA_SEL_OWN_FIRST) { K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1; kk = 1 + K; }
   else { K = d->topk < d->nblk ? d->topk : d->nblk; kk = K + 1 + (d->sink ? 1 : 0); }
   if (d->kk != kk) return fail(FBSA_EINVAL, "fbsa_select: kk=%lld but the convention gives %lld", (long long)d->kk, (long long)kk);
-  if (K > 62) return fail(FBSA_EUNSUPPORTED, "fbsa_select: top-k budget %lld > 62 is not supported", (long long)K);
+  if (K > kSelWideMax)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_select: top-k budget %lld > %lld is not supported", (long long)K,
+                (long long)kSelWideMax);
   if (!a || !b1 || !sel || (d->score != FBSA_SCORE_DOT && !b2)) return fail(FBSA_EINVAL, "fbsa_select: null pointer");
   const int64_t es = esize(d->dtype);
   if (!aligned(a, es) || !aligned(b1, 16) || (b2 && !aligned(b2, 16)) || !aligned(sel, 4) || (sel_score && !aligned(sel_score, 4)))

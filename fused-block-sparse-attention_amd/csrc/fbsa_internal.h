@@ -24,6 +24,11 @@ struct FwdArgs {
   int dense;     // FBSA_FLAG_DENSE: slot s is block s, sel and gate unused
 };
 
+// Top-k budgets of fbsa_select: up to kSelListMax on the wave-list kernels,
+// up to kSelWideMax on the row-per-workgroup kernel (its keys live in LDS).
+constexpr int64_t kSelListMax = 62;
+constexpr int64_t kSelWideMax = 4096;
+
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
 int run_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float *mass, float *lse, hipStream_t s);

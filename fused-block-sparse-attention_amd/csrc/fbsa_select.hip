@@ -642,6 +642,137 @@ __global__ __launch_bounds__(256) void select_kernel(SelArgs a) {
   }
 }
 
+// ------------------------------------------------ wide top-k (K > 62)
+//
+// Budgets past one wave-wide list: one workgroup per (batch, head, query row).
+// Candidates are scored exactly as in select_kernel (fp64 dot products in
+// dimension order, rounded where torch rounds) in tiles of KP, where KP is a
+// power of two >= max(K, 256). LDS holds the row's best keys so far (sorted,
+// descending; 0 = empty) followed by the tile; a tile with no key above the
+// current K-th is skipped, otherwise the 2 KP keys are sorted (bitonic network)
+// and the first KP kept. Keys order as in the other kernels (score, then the
+// lower block index), so the chosen blocks are the same.
+__device__ __forceinline__ void bitonic_desc_u64(uint64_t *v, int n, int tid) {
+  for (int k = 2; k <= n; k <<= 1)
+    for (int jj = k >> 1; jj > 0; jj >>= 1) {
+      for (int x = tid; x < n; x += 256) {
+        const int y = x ^ jj;
+        if (y > x) {
+          const uint64_t p = v[x], q = v[y];
+          const bool desc = (x & k) == 0;
+          if (desc ? p < q : p > q) { v[x] = q; v[y] = p; }
+        }
+      }
+      __syncthreads();
+    }
+}
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void select_wide_kernel(SelArgs a, int KP) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  uint64_t *buf = (uint64_t *)smem;                     // [2 KP] best keys | tile
+  double *qa = (double *)(buf + 2 * KP);                // [2][D] query operand (QUEST: relu / negative parts)
+  float *osc = (float *)(qa + 2 * D);                   // [KP + 2] scores of the output slots
+  __shared__ float s_diag, s_sink;
+  const int tid = threadIdx.x;
+  const int64_t nrows = a.row1 - a.row0;
+  const int64_t bh = blockIdx.x / nrows;
+  const int64_t i = a.row1 - 1 - (int64_t)blockIdx.x % nrows;  // later (longer) rows first
+  const T *A = (const T *)a.a + bh * a.nblk * D;
+  const T *B1 = (const T *)a.b1 + bh * a.nblk * D;
+  const T *B2 = MODE != FBSA_SCORE_DOT ? (const T *)a.b2 + bh * a.nblk * D : nullptr;
+  for (int d = tid; d < D; d += 256) {
+    const double v = (double)(float)A[i * D + d];
+    if (MODE == FBSA_SCORE_QUEST) { qa[d] = v > 0.0 ? v : 0.0; qa[D + d] = v < 0.0 ? v : 0.0; }
+    else qa[d] = v;
+  }
+  for (int x = tid; x < KP; x += 256) buf[x] = 0;
+  __syncthreads();
+  auto score = [&](int64_t j) {
+    double acc = 0.0, acc2 = 0.0;
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      double bv[8], bv2[8];
+      load8<T>(B1 + j * D + d0, bv);
+      if (MODE != FBSA_SCORE_DOT) load8<T>(B2 + j * D + d0, bv2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (MODE == FBSA_SCORE_QUEST) {
+          acc = __builtin_fma(qa[d0 + e], bv[e], acc);
+          acc2 = __builtin_fma(qa[D + d0 + e], bv2[e], acc2);
+        } else {
+          acc = __builtin_fma(qa[d0 + e], bv[e], acc);
+          if (MODE == FBSA_SCORE_MAX2) acc2 = __builtin_fma(qa[d0 + e], bv2[e], acc2);
+        }
+      }
+    }
+    if (MODE == FBSA_SCORE_DOT) return round_dt<T>(acc);
+    if (MODE == FBSA_SCORE_MAX2) return fmaxf(round_dt<T>(acc), round_dt<T>(acc2));
+    return round_dt_f<T>(round_dt<T>(acc) + round_dt<T>(acc2));
+  };
+  if (tid == 0) s_diag = score(i);
+  if (tid == 64) s_sink = score(0);
+  const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
+  const int K = (int)(convA ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1) : (a.topk < a.nblk ? a.topk : a.nblk));
+  const int64_t jmax = (a.causal || !convA) ? i : a.nblk - 1;
+  for (int64_t t0 = 0; t0 <= jmax; t0 += KP) {
+    const uint64_t kth = buf[K - 1];  // stable: the previous tile ended with a barrier
+    int any = 0;
+    for (int x = tid; x < KP; x += 256) {
+      const int64_t j = t0 + x;
+      uint64_t key = 0;
+      if (j <= jmax && (convA ? (a.causal ? j < i : j != i) : true)) {
+        key = make_key(score(j), (int)j);
+        if (key <= kth) key = 0;
+      }
+      buf[KP + x] = key;
+      any |= key != 0;
+    }
+    if (!__syncthreads_or(any)) continue;
+    bitonic_desc_u64(buf, 2 * KP, tid);
+  }
+  __syncthreads();
+  int32_t *srow = a.sel + (bh * a.nblk + i) * a.kk;
+  float *scrow = a.sel_score ? a.sel_score + (bh * a.nblk + i) * a.kk : nullptr;
+  const float dsc = s_diag;
+  if (convA) {
+    // slot 0 = own block, slots 1..K in score order; missing picks -> own
+    for (int s = tid; s < a.kk; s += 256) {
+      int idx = (int)i;
+      float sc = dsc;
+      if (s >= 1 && buf[s - 1] != 0) { idx = key_index(buf[s - 1]); sc = key_score(buf[s - 1]); }
+      srow[s] = idx;
+      if (scrow) scrow[s] = sc;
+    }
+    return;
+  }
+  // _finish: K picks (non-finite or missing -> own), own, sink; sorted ascending
+  // (by block, then slot: keys block << 32 | slot into the free tile half)
+  const int n = (int)a.kk;
+  for (int s = tid; s < n; s += 256) {
+    int idx = (int)i;
+    float sc = dsc;
+    if (s < K) {
+      const uint64_t kv = buf[s];
+      if (kv != 0 && isfinite(key_score(kv))) { idx = key_index(kv); sc = key_score(kv); }
+    } else if (s == K + 1) {
+      idx = 0;
+      sc = s_sink;
+    }
+    osc[s] = sc;
+    buf[KP + s] = ((uint64_t)(uint32_t)idx << 32) | (uint32_t)s;
+  }
+  int np = 1;
+  while (np < n) np <<= 1;
+  for (int s = n + tid; s < np; s += 256) buf[KP + s] = 0;  // empties sort last in descending order
+  __syncthreads();
+  bitonic_desc_u64(buf + KP, np, tid);
+  for (int s = tid; s < n; s += 256) {
+    const uint64_t kv = buf[KP + n - 1 - s];  // ascending
+    srow[s] = (int32_t)(kv >> 32);
+    if (scrow) scrow[s] = osc[(uint32_t)kv];
+  }
+}
+
 // ------------------------------------------------ MFMA selection (16-bit operands)
 //
 // Scores come from bf16/fp16 MFMA (fp32 accumulate). With exact 16-bit
@@ -1536,6 +1667,24 @@ template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, v
       hipLaunchKernelGGL((select_merge_kernel<T, D, MODE>), dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, b);
       return hip_check(hipGetLastError(), "select_merge_kernel launch");
     }
+  }
+  const bool convA = a.conv == FBSA_SEL_OWN_FIRST;
+  const int64_t K = convA ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1) : (a.topk < a.nblk ? a.topk : a.nblk);
+  if (K > kSelListMax) {
+    int KP = 256;
+    while (KP < K) KP <<= 1;
+    const size_t lds = (size_t)2 * KP * 8 + (size_t)2 * D * 8 + (size_t)(KP + 2) * 4;
+    static size_t granted = 0;
+    if (lds > 64 * 1024 && lds > granted) {
+      int e = hip_check(hipFuncSetAttribute((const void *)select_wide_kernel<T, D, MODE>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                        "hipFuncSetAttribute(select_wide)");
+      if (e) return e;
+      granted = lds;
+    }
+    const int64_t nwg = (a.row1 - a.row0) * a.B * a.H;
+    hipLaunchKernelGGL((select_wide_kernel<T, D, MODE>), dim3((unsigned)nwg), dim3(256), lds, s, a, KP);
+    return hip_check(hipGetLastError(), "select_wide_kernel launch");
   }
   constexpr int R = 8;
   const int64_t ntile = (a.row1 - a.row0 + R - 1) / R;

@@ -15,7 +15,7 @@ POOL_OPS = {"mean_tok_then_grp": _lib.POOL_MEAN_TOK_THEN_GRP,
             "mean_grp_then_tok": _lib.POOL_MEAN_GRP_THEN_TOK,
             "max": _lib.POOL_MAX, "min": _lib.POOL_MIN, "minmax": _lib.POOL_MINMAX}
 SCORES = {"dot": _lib.SCORE_DOT, "max2": _lib.SCORE_MAX2, "quest": _lib.SCORE_QUEST}
-MAX_TOPK = 62  # largest top-k budget of the streaming selection kernel (one wave-wide list)
+MAX_TOPK = 4096  # largest top-k budget of fbsa_select (past 62: one workgroup per row, keys in LDS)
 
 
 def pool(x, bs, op, grp=1, l_valid=None):

@@ -151,7 +151,9 @@ typedef struct fbsa_select_desc {
 
 /* Streaming score + top-k: writes sel (B,H,nblk,kk) int32 and, when sel_score
  * != NULL, the score of each chosen slot as fp32 (for the log-sigmoid gate).
- * Ties break towards the lower block index. With a workspace of at least
+ * Ties break towards the lower block index. Top-k budgets up to 62 run on
+ * wave-wide lists; larger ones (up to 4096) on one workgroup per query row
+ * with the row's keys in LDS (same scores, same result). With a workspace of at least
  * fbsa_select_workspace_bytes() bytes (16-byte aligned; nonzero for 16-bit
  * operands of dim >= 32) scores are formed on MFMA and verified exactly (fp64
  * only where the rounding is ambiguous); without one, every score is formed

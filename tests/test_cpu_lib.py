@@ -84,8 +84,10 @@ def test_select_rejects_bad_budget():
     d.B, d.H, d.nblk, d.D, d.topk, d.kk = 1, 1, 64, 64, 8, 8   # convention A needs kk = 9
     assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EINVAL
     assert "kk" in lib.fbsa_last_error().decode()
-    d.kk, d.topk = 64, 63
+    # budgets past the wave lists run one workgroup per row, up to 4096
+    d.nblk, d.topk, d.kk = 8192, 4097, 4098
     assert lib.fbsa_select(d, DUMMY, DUMMY, None, DUMMY, None, None, 0, None) == _lib.EUNSUPPORTED
+    assert "4096" in lib.fbsa_last_error().decode()
 
 
 def test_select_flags_and_workspace_size():

@@ -245,3 +245,53 @@ def test_select_tiled_modes(dtype, D, score, conv, causal, topk, ties, chunk):
         ref = osel.select_conv_b(raw, topk, sink)
     _check_sel(sel.cpu().numpy(), ref, "sel")
     assert np.array_equal(sc.cpu().numpy().astype(np.float64), np.take_along_axis(raw, ref, -1))
+
+
+@pytest.mark.parametrize("dtype,score,conv,causal,topk,nblk,ties", [
+    ("bf16", "dot", "own_first", True, 64, 900, False),
+    ("bf16", "dot", "own_first", True, 128, 900, True),
+    ("bf16", "dot", "own_first", False, 63, 300, False),
+    ("f32", "dot", "own_first", True, 128, 600, False),
+    ("bf16", "max2", "own_first", True, 100, 700, False),
+    ("bf16", "dot", "sorted_sink", True, 64, 900, True),
+    ("f16", "quest", "sorted_sink", True, 128, 700, False),
+    ("bf16", "dot", "sorted_sink", True, 700, 700, False),
+    ("bf16", "quest", "sorted_sink", True, 300, 1200, True),
+])
+def test_select_wide_budgets(dtype, score, conv, causal, topk, nblk, ties):
+    # top-k budgets past one wave-wide list (> 62): one workgroup per row with
+    # its keys in LDS; blocks and chosen-slot scores bit-exact against the oracle
+    # (src/ssa_model.py:158-161 and src/qwen_blocksparse.py:90 take any topk)
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(31)
+    B, H, D = 1, 2, 64
+    if ties:
+        mk = lambda: torch.randint(-2, 3, (B, H, nblk, D), generator=g).to(torch.bfloat16 if dtype == "bf16" else torch.float16 if dtype == "f16" else torch.float32)  # noqa: E731
+    else:
+        mk = lambda: randn(g, (B, H, nblk, D), dtype)  # noqa: E731
+    a, b1, b2 = mk(), mk(), mk()
+    if score == "quest":
+        b1, b2 = torch.maximum(b1, b2), torch.minimum(b1, b2)
+    _say("wide", dtype, score, conv, causal, topk, nblk, ties)
+    sel, sc = selection.select(a.to(DEV), b1.to(DEV), None if score == "dot" else b2.to(DEV), score=score,
+                               convention=conv, topk=topk, causal=causal, sink=conv == "sorted_sink",
+                               need_scores=True)
+    raw = osel.scores(np64(a), np64(b1), dtype, score, b2=None if score == "dot" else np64(b2))
+    if conv == "own_first":
+        ref = np.stack([osel.select_conv_a(raw[:, h], topk, causal) for h in range(H)], 1)
+    else:
+        ref = osel.select_conv_b(raw, topk, True)
+    _check_sel(sel.cpu().numpy(), ref, "sel")
+    assert np.array_equal(sc.cpu().numpy().astype(np.float64), np.take_along_axis(raw, ref, -1))
+
+
+def test_select_quest_topk_100_config4_rows():
+    # SelectMax with a budget of 100 at D 256 (the row-per-workgroup Quest kernel)
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(32)
+    B, Hq, Hkv, N, D, bs, topk = 1, 4, 2, 128 * 300, 256, 128, 100
+    q = randn(g, (B, Hq, N, D), "bf16")
+    k = randn(g, (B, Hkv, N, D), "bf16")
+    idx = selection.select_quest(q.to(DEV), k.to(DEV), bs, topk, sink=True).cpu().numpy()
+    ref, _ = osel.select_quest(np64(q), np64(k), bs, topk, True, "bf16")
+    _check_sel(idx, ref, "idx")
