@@ -5,7 +5,7 @@
 //   1. prep_kernel     per query row: delta = sum_d dO*O and lse*log2(e)
 //                      (rowstat); with an output gate also dO*sigmoid(g) and
 //                      the gate gradient dO*O*(1 - sigmoid(g)).
-//   2. keys_kernel + stable radix sort + seg_off_kernel
+//   2. keys_kernel + stable radix sort (rocPRIM) + seg_off_kernel
 //                      the block-transposed index: for each (b, hsel, key
 //                      block j) the valid (i, slot) pairs that read block j,
 //                      ascending, as a CSR.
@@ -30,7 +30,8 @@
 // dS = P (dP - D), dQ = dS K scale, dK = dS^T Q scale, dV = P^T dO), the
 // token-causal/padding/duplicate masks of src/qwen_blocksparse.py:67-72, and
 // the gate gradient the gather path (src/ssa_model.py:72-74) gives.
-#include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
 
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
@@ -97,9 +98,9 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   while (((int64_t)1 << bits) <= lay->nseg) ++bits;
   lay->end_bit = bits;
   size_t tmp = 0;
-  hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, tmp, (const uint32_t *)nullptr, (uint32_t *)nullptr,
-                                                    (const int32_t *)nullptr, (int32_t *)nullptr, (int)lay->n, 0,
-                                                    bits, (hipStream_t)0);
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, tmp, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+                                           (const int32_t *)nullptr, (int32_t *)nullptr, (unsigned)lay->n, 0u,
+                                           (unsigned)bits, (hipStream_t)0);
   if (e != hipSuccess) return hip_check(e, "radix sort workspace query");
   lay->sort_tmp_bytes = tmp;
   const size_t rows = (size_t)(d->B * d->Hq * d->L);
@@ -136,8 +137,8 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
     lay->xub = walked / segE + 1;
     lay->slots_ub = 2 * (walked / segE) + 1;
     size_t stmp = 0;
-    e = hipcub::DeviceScan::ExclusiveSum(nullptr, stmp, (const uint64_t *)nullptr, (uint64_t *)nullptr,
-                                         (int)(lay->nwi + 1), (hipStream_t)0);
+    e = rocprim::exclusive_scan(nullptr, stmp, (const uint64_t *)nullptr, (uint64_t *)nullptr, (uint64_t)0,
+                                (size_t)(lay->nwi + 1), rocprim::plus<uint64_t>(), (hipStream_t)0);
     if (e != hipSuccess) return hip_check(e, "scan workspace query");
     lay->scan_tmp_bytes = stmp;
     lay->seg_cnt = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
@@ -355,9 +356,9 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
   int e = hip_check(hipGetLastError(), "keys_kernel launch");
   if (e) return e;
   size_t tmp = lay.sort_tmp_bytes;
-  e = hip_check(hipcub::DeviceRadixSort::SortPairs(ws + lay.sort_tmp, tmp, (const uint32_t *)(ws + lay.keys_in),
-                                                   (uint32_t *)(ws + lay.keys_out), (const int32_t *)(ws + lay.vals_in),
-                                                   (int32_t *)(ws + lay.vals_out), (int)lay.n, 0, lay.end_bit, s),
+  e = hip_check(rocprim::radix_sort_pairs(ws + lay.sort_tmp, tmp, (const uint32_t *)(ws + lay.keys_in),
+                                          (uint32_t *)(ws + lay.keys_out), (const int32_t *)(ws + lay.vals_in),
+                                          (int32_t *)(ws + lay.vals_out), (unsigned)lay.n, 0u, (unsigned)lay.end_bit, s),
                 "radix sort of the transposed index");
   if (e) return e;
   hipLaunchKernelGGL(seg_off_kernel, dim3((unsigned)((lay.nseg + 1 + 255) / 256)), dim3(256), 0, s,
@@ -1130,8 +1131,8 @@ int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, c
                        (const int32_t *)(ws + lay.seg_off), lay.nwi, d->nblk, d->Hkv, d->hsel, lay.seg_entries, cnt);
     if ((e = hip_check(hipGetLastError(), "seg_count_kernel launch"))) return e;
     size_t tmp = lay.scan_tmp_bytes;
-    if ((e = hip_check(hipcub::DeviceScan::ExclusiveSum(ws + lay.scan_tmp, tmp, (const uint64_t *)cnt, pos,
-                                                        (int)(lay.nwi + 1), s),
+    if ((e = hip_check(rocprim::exclusive_scan(ws + lay.scan_tmp, tmp, (const uint64_t *)cnt, pos, (uint64_t)0,
+                                               (size_t)(lay.nwi + 1), rocprim::plus<uint64_t>(), s),
                        "scan of the list segments")))
       return e;
     hipLaunchKernelGGL(seg_table_kernel, dim3((unsigned)((lay.nwi + 255) / 256)), dim3(256), 0, s,
