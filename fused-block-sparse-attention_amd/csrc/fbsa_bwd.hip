@@ -44,6 +44,10 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_DQ_LDS_BUDGET
 #define FBSA_DQ_LDS_BUDGET 32768
 #endif
+// work chunks (KC query rows of one reading query block and head) per dK/dV list segment
+#ifndef FBSA_SEG_CHUNKS
+#define FBSA_SEG_CHUNKS 512
+#endif
 #ifndef FBSA_DKDV_LDS_BUDGET
 #define FBSA_DKDV_LDS_BUDGET 40960
 #endif
@@ -120,7 +124,7 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   // the rounding of sums over ~1e5 query rows under 1e-4 of the result's scale)
   const int64_t grp = d->Hq / d->Hkv;
   const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
-  int64_t segE = (d->dtype == FBSA_F32 ? 512 : 4096) / (grp * (d->bs / kc));
+  int64_t segE = (d->dtype == FBSA_F32 ? 512 : FBSA_SEG_CHUNKS) / (grp * (d->bs / kc));
   if (segE < 16) segE = 16;
   lay->nwi = d->B * d->Hkv * d->nblk;
   if (lay->nwi >= 0x7fffffffLL)
@@ -406,7 +410,7 @@ template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
 };
 
-template <typename T, int BS, int D>
+template <typename T, int BS, int D, bool DENSE = false>
 __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -430,9 +434,9 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 
   // plan: compact list of valid slots (same rule as the forward; dense: implicit)
   const int64_t rowoff = ((b * a.hsel + hs) * a.nblk + i) * a.kk;
-  const int32_t *selrow = a.dense ? nullptr : a.sel + rowoff;
+  const int32_t *selrow = DENSE ? nullptr : a.sel + rowoff;
   const int nkb = (int)((a.l_valid + BS - 1) / BS);  // key blocks holding a valid key
-  if (!a.dense && w == 0) {
+  if (!DENSE && w == 0) {
     int nout = 0;
     for (int s0 = 0; s0 < a.kk; s0 += 64) {
       const int s = s0 + lane;
@@ -474,11 +478,11 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
   const float2 rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
   const float lse2 = rs.x, delta = rs.y;
   __syncthreads();
-  const int nv = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
+  const int nv = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
-  auto blk_of = [&](int slot) { return a.dense ? slot : s_blk[slot]; };
+  auto blk_of = [&](int slot) { return DENSE ? slot : s_blk[slot]; };
   auto kind_of = [&](int slot) {
-    if (!a.dense) return s_kind[slot];
+    if (!DENSE) return s_kind[slot];
     const int64_t jj = slot;
     const bool pad = (jj + 1) * BS > a.l_valid;
     return a.mask == FBSA_MASK_TOKEN_CAUSAL ? ((jj == i || pad) ? (int)KIND_ABS : (int)KIND_FULL)
@@ -521,7 +525,7 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     const char *Vs = Ks + C::TILE_BYTES;
     const int slot = c / C::NCH, ch = c % C::NCH;
     const int kind = kind_of(slot);
-    const float gt = a.dense ? 0.f : s_gate[slot];
+    const float gt = DENSE ? 0.f : s_gate[slot];
     const int64_t j = blk_of(slot);
 
     f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
@@ -624,7 +628,7 @@ using DkdvCfg = BwdCfg<T, BS, D,
 // exponentials), so occupancy decides: for bs 64 with 16-bit d <= 64 the
 // kernel is held to four waves per SIMD (at most 128 VGPRs) and its two-stage
 // ring (35 KB of LDS) fits four workgroups per CU.
-template <typename T, int BS, int D>
+template <typename T, int BS, int D, bool DENSE = false>
 __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>())) void dkdv_kernel(BwdArgs a) {
   using C = DkdvCfg<T, BS, D>;
   constexpr int ROLES = dkdv_roles<T, D>(), KEYS = dkdv_keys<T, BS, D>();
@@ -715,14 +719,14 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   }
 
   // dense lists: entry at position e of block j's list is query block dense_i0 + e
-  const int64_t dense_i0 = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL ? j : 0) - a.seg_off[seg] : 0;
+  const int64_t dense_i0 = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL ? j : 0) - a.seg_off[seg] : 0;
   for (int eb = e0; eb < e1; eb += MAXE) {
     const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
     __syncthreads();  // the previous batch's entries are no longer read
     for (int x = tid; x < ne; x += C::NT) {
       // dense: the list of block j is query blocks j.. (causal) or 0.., slot j
       int i, s;
-      if (a.dense) {
+      if (DENSE) {
         i = (int)(dense_i0 + eb + x);
         s = (int)j;
       } else {
@@ -1050,27 +1054,36 @@ template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, co
   return FBSA_OK;
 }
 
-template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipStream_t s) {
+template <typename T, int BS, int D, bool DENSE> static int launch_dq_as(const BwdArgs &a, hipStream_t s) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (a.dense ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
   static size_t granted = 0;
-  int e = set_lds(dq_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dq");
+  int e = set_lds(dq_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dq");
   if (e) return e;
-  hipLaunchKernelGGL((dq_kernel<T, BS, D>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((dq_kernel<T, BS, D, DENSE>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dq_kernel launch");
 }
 
-template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
+template <typename T, int BS, int D, bool DENSE> static int launch_dkdv_as(const BwdArgs &a, hipStream_t s) {
   using C = DkdvCfg<T, BS, D>;
   constexpr int HR = C::KC >= 64 ? 32 : C::KC;
   const size_t xch = dkdv_roles<T, D>() == 2 ? (size_t)(dkdv_keys<T, BS, D>() / 16) * 64 * (HR / 16) * 16 : 0;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16 + xch;
   static size_t granted = 0;
-  int e = set_lds(dkdv_kernel<T, BS, D>, lds, granted, "fbsa_bwd_dkdv");
+  int e = set_lds(dkdv_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dkdv");
   if (e) return e;
   const int64_t nwg = (a.B * a.Hkv * a.nblk + (a.wi_slot ? a.seg_entries_xub : 0)) * (BS / dkdv_keys<T, BS, D>());
-  hipLaunchKernelGGL((dkdv_kernel<T, BS, D>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((dkdv_kernel<T, BS, D, DENSE>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dkdv_kernel launch");
+}
+
+// the dense (list-less) forms are their own instantiations (the list path's
+// code is unchanged by them)
+template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipStream_t s) {
+  return a.dense ? launch_dq_as<T, BS, D, true>(a, s) : launch_dq_as<T, BS, D, false>(a, s);
+}
+template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
+  return a.dense ? launch_dkdv_as<T, BS, D, true>(a, s) : launch_dkdv_as<T, BS, D, false>(a, s);
 }
 
 template <typename T, int BS> static int bwd_d(const BwdArgs &a, int64_t D, bool dq, hipStream_t s) {

@@ -62,7 +62,7 @@ template <int N> __device__ __forceinline__ void wait_pending(int pending_chunks
   }
 }
 
-template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0, bool DENSE = false>
 __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
   constexpr bool F32 = sizeof(T) == 4;
@@ -90,9 +90,9 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   // (dense: slot s is block s for the blocks below l_valid, and up to i when
   // causal; kinds follow from the block index, no table)
   const int64_t rowoff = ((b * a.hsel + hs) * a.nblk + i) * a.kk;
-  const int32_t *selrow = a.dense ? nullptr : a.sel + rowoff;
+  const int32_t *selrow = DENSE ? nullptr : a.sel + rowoff;
   const int nkb = (int)((a.l_valid + BS - 1) / BS);  // key blocks holding a valid key
-  if (!a.dense && w == 0) {
+  if (!DENSE && w == 0) {
     int nout = 0;
     for (int s0 = 0; s0 < a.kk; s0 += 64) {
       const int s = s0 + lane;
@@ -160,11 +160,11 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     doff[n] = (int32_t)(((int64_t)row * (part ? a.sv[2] : a.sk[2]) + chunk * (16 / C::ES)) * C::ES);
   }
   __syncthreads();
-  const int nv = a.dense ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
+  const int nv = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
-  auto blk_of = [&](int slot) { return a.dense ? slot : s_blk[slot]; };
+  auto blk_of = [&](int slot) { return DENSE ? slot : s_blk[slot]; };
   auto kind_of = [&](int slot) {
-    if (!a.dense) return s_kind[slot];
+    if (!DENSE) return s_kind[slot];
     const int64_t jj = slot;
     const bool pad = (jj + 1) * BS > a.l_valid;
     return a.mask == FBSA_MASK_TOKEN_CAUSAL ? ((jj == i || pad) ? (int)KIND_ABS : (int)KIND_FULL)
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     const char *Vs = Ks + C::TILE_BYTES;
     const int slot = c / C::NCH, ch = c % C::NCH;
     const int kind = kind_of(slot);
-    const float gt = a.dense ? 0.f : s_gate[slot];
+    const float gt = DENSE ? 0.f : s_gate[slot];
     const int64_t j = blk_of(slot);
 
     // V^T fragments for the PV product, shared by the query tiles; issued first
@@ -432,15 +432,15 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   }
 }
 
-template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
-static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0, bool DENSE = false>
+static int launch_fwd_as(const FwdArgs &a, hipStream_t stream) {
   using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (a.dense ? 0 : (size_t)a.kk * 12);
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 12);
   if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: kk=%lld needs %zu bytes of LDS", (long long)a.kk, lds);
   if (lds > 64 * 1024) {
     static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation
     if (lds > attr_bytes) {
-      int e = hip_check(hipFuncSetAttribute((const void *)fwd_kernel<T, BS, D, QT, KCO, NSO>,
+      int e = hip_check(hipFuncSetAttribute((const void *)fwd_kernel<T, BS, D, QT, KCO, NSO, DENSE>,
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                         "hipFuncSetAttribute(fwd)");
       if (e) return e;
@@ -449,8 +449,16 @@ static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
   }
   const int64_t nwg = a.B * a.Hq * a.ni;
   if (nwg == 0) return FBSA_OK;
-  hipLaunchKernelGGL((fwd_kernel<T, BS, D, QT, KCO, NSO>), dim3((unsigned)nwg), dim3(C::NT), lds, stream, a);
+  hipLaunchKernelGGL((fwd_kernel<T, BS, D, QT, KCO, NSO, DENSE>), dim3((unsigned)nwg), dim3(C::NT), lds, stream, a);
   return hip_check(hipGetLastError(), "fwd_kernel launch");
+}
+
+// the dense (list-less) form is its own instantiation, so the list path's code
+// is unchanged by it
+template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0>
+static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
+  return a.dense ? launch_fwd_as<T, BS, D, QT, KCO, NSO, true>(a, stream)
+                 : launch_fwd_as<T, BS, D, QT, KCO, NSO, false>(a, stream);
 }
 
 template <typename T, int BS> static int dispatch_d(const FwdArgs &a, int64_t D, hipStream_t s) {
