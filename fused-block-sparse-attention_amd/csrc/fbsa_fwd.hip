@@ -50,6 +50,33 @@ template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0> struc
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
 };
 
+// K fragments requested all at once before the score MFMAs (16-bit types)
+#ifndef FBSA_FWD_KFIRST
+#define FBSA_FWD_KFIRST 1
+#endif
+
+// lgkmcnt wait for a count known after unrolling (values above 15 wait for 15)
+__device__ __forceinline__ void lds_wait_upto(int n) {
+  switch (n < 15 ? n : 15) {
+    case 0: lds_wait_le<0>(); break;
+    case 1: lds_wait_le<1>(); break;
+    case 2: lds_wait_le<2>(); break;
+    case 3: lds_wait_le<3>(); break;
+    case 4: lds_wait_le<4>(); break;
+    case 5: lds_wait_le<5>(); break;
+    case 6: lds_wait_le<6>(); break;
+    case 7: lds_wait_le<7>(); break;
+    case 8: lds_wait_le<8>(); break;
+    case 9: lds_wait_le<9>(); break;
+    case 10: lds_wait_le<10>(); break;
+    case 11: lds_wait_le<11>(); break;
+    case 12: lds_wait_le<12>(); break;
+    case 13: lds_wait_le<13>(); break;
+    case 14: lds_wait_le<14>(); break;
+    default: lds_wait_le<15>(); break;
+  }
+}
+
 template <int N> __device__ __forceinline__ void wait_pending(int pending_chunks) {
   // wait until at most pending_chunks * LPT DMA loads are outstanding (N = LPT)
   switch (pending_chunks) {
@@ -228,11 +255,10 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     const float gt = DENSE ? 0.f : s_gate[slot];
     const int64_t j = blk_of(slot);
 
-    // V^T fragments for the PV product, shared by the query tiles; issued first
-    // so their LDS latency overlaps the score MFMAs and the softmax
+    // V^T fragments for the PV product, shared by the query tiles (16-bit types)
     constexpr int KV2 = C::KC >= 32 ? C::KC / 32 : 1;
     s16x4 vlo[F32 ? 1 : D / 16][KV2], vhi[F32 ? 1 : D / 16][KV2];
-    if constexpr (!F32) {
+    auto read_v = [&]() {
 #pragma unroll
       for (int mt = 0; mt < D / 16; ++mt) {
         const int cb = 2 * mt + ((p & 3) >> 1);  // logical 16-B chunk of d0 = 16mt + 4(p&3)
@@ -246,23 +272,54 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
           }
         }
       }
-    }
+    };
 
     // S^T (KC keys x 16 queries per tile); each K fragment feeds every tile
     f32x4 sacc[QT][C::KC / 16];
 #pragma unroll
-    for (int m = 0; m < C::KC / 16; ++m) {
+    for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * m + p;
-      if constexpr (F32) {
+    if constexpr (F32) {
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m) {
+        const int row = 16 * m + p;
 #pragma unroll
         for (int ks = 0; ks < QF; ++ks) {
           const float kf = *(const float *)(Ks + (row * C::CPR + (ks ^ swz(row, C::CPR))) * 16 + g * 4);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = mfma_f32_16x16x4(kf, qf32[qt][ks], sacc[qt][m]);
         }
-      } else {
+      }
+    } else if constexpr (FBSA_FWD_KFIRST) {
+      // every K fragment of the chunk is requested at once and each MFMA waits
+      // only for its own (LDS reads complete in order); the V^T reads follow,
+      // so their latency overlaps the MFMAs in flight and the softmax
+      constexpr int NK = C::KC / 16 * QF;
+      s16x8 kf[C::KC / 16][QF];
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int ks = 0; ks < QF; ++ks) {
+          const int row = 16 * m + p;
+          kf[m][ks] = lds_read_b128(Ks + (row * C::CPR + ((4 * ks + g) ^ swz(row, C::CPR))) * 16);
+        }
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int ks = 0; ks < QF; ++ks) {
+          lds_wait_upto(NK - 1 - (m * QF + ks));
+          lds_ready(kf[m][ks]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = Mfma16<T>::run(kf[m][ks], qf16[qt][ks], sacc[qt][m]);
+        }
+      read_v();
+    } else {
+      // V^T requested first, so its LDS latency overlaps the score MFMAs
+      read_v();
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m) {
+        const int row = 16 * m + p;
 #pragma unroll
         for (int ks = 0; ks < QF; ++ks) {
           const s16x8 kf = *(const s16x8 *)(Ks + (row * C::CPR + ((4 * ks + g) ^ swz(row, C::CPR))) * 16);
@@ -461,12 +518,22 @@ static int launch_fwd(const FwdArgs &a, hipStream_t stream) {
                  : launch_fwd_as<T, BS, D, QT, KCO, NSO, false>(a, stream);
 }
 
+// query tiles per wave at d = 256 (16-bit types, blocks of 64 or more rows)
+#ifndef FBSA_FWD_QT256
+#define FBSA_FWD_QT256 1
+#endif
+#ifndef FBSA_FWD_NS256
+#define FBSA_FWD_NS256 0
+#endif
+
 template <typename T, int BS> static int dispatch_d(const FwdArgs &a, int64_t D, hipStream_t s) {
+  constexpr int QT256 = (sizeof(T) == 2 && BS >= 64) ? FBSA_FWD_QT256 : 1;
+  constexpr int NS256 = (sizeof(T) == 2 && BS >= 64) ? FBSA_FWD_NS256 : 0;
   switch (D) {
     case 32: return launch_fwd<T, BS, 32>(a, s);
     case 64: return launch_fwd<T, BS, 64>(a, s);
     case 128: return launch_fwd<T, BS, 128>(a, s);
-    case 256: return launch_fwd<T, BS, 256>(a, s);
+    case 256: return launch_fwd<T, BS, 256, QT256, 0, NS256>(a, s);
   }
   return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: head dim %lld not in {32,64,128,256}", (long long)D);
 }
