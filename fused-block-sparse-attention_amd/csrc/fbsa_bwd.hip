@@ -44,6 +44,15 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_DQ_LDS_BUDGET
 #define FBSA_DQ_LDS_BUDGET 32768
 #endif
+// LDS reads in flight per row product (16-bit types, d >= 128; 0 = compiler-
+// scheduled, kept for d <= 64 where the window would cost occupancy)
+#ifndef FBSA_DQ_WIN
+#define FBSA_DQ_WIN 8
+#endif
+#ifndef FBSA_DKDV_WIN
+#define FBSA_DKDV_WIN 8
+#endif
+
 // work chunks (KC query rows of one reading query block and head) per dK/dV list segment
 #ifndef FBSA_SEG_CHUNKS
 #define FBSA_SEG_CHUNKS 512
@@ -529,8 +538,8 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     const int64_t j = blk_of(slot);
 
     f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
-    mm_rows_frag<T, D, C::KC / 16>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
-    mm_rows_frag<T, D, C::KC / 16>(Vs, df, dpacc, g, p);  // dP^T
+    mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
+    mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Vs, df, dpacc, g, p);  // dP^T
 
     int lim = 1 << 30;
     if (kind != KIND_FULL) {
@@ -819,7 +828,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         const int th = tmin - h * HR;
         if constexpr (ROLES == 2) {
           f32x4 xacc[HR / 16];
-          mm_rows_frag<T, D, HR / 16>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
           float4 *xs = s_xch + (kw * 64 + lane) * (HR / 16);
           float x[HR / 16][4];
           if (role == 0) {
@@ -852,8 +861,8 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
           continue;
         }
         f32x4 sacc[HR / 16], dpacc[HR / 16];
-        mm_rows_frag<T, D, HR / 16>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
-        mm_rows_frag<T, D, HR / 16>(Dh, vf, dpacc, g, p);  // dP
+        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
+        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p);  // dP
         float pp[HR / 16][4], ds[HR / 16][4];
         // every exponential is computed and masked by a select: a conditional
         // exponential becomes a branch per element, each waiting for its own

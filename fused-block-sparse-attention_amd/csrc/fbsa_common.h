@@ -133,6 +133,28 @@ template <int N> __device__ __forceinline__ void lds_wait_le() {
   static_assert(N >= 0 && N <= 15, "lgkmcnt range");
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
 }
+// lgkmcnt wait for a count known after unrolling (values above 15 wait for 15)
+__device__ __forceinline__ void lds_wait_upto(int n) {
+  switch (n < 15 ? n : 15) {
+    case 0: lds_wait_le<0>(); break;
+    case 1: lds_wait_le<1>(); break;
+    case 2: lds_wait_le<2>(); break;
+    case 3: lds_wait_le<3>(); break;
+    case 4: lds_wait_le<4>(); break;
+    case 5: lds_wait_le<5>(); break;
+    case 6: lds_wait_le<6>(); break;
+    case 7: lds_wait_le<7>(); break;
+    case 8: lds_wait_le<8>(); break;
+    case 9: lds_wait_le<9>(); break;
+    case 10: lds_wait_le<10>(); break;
+    case 11: lds_wait_le<11>(); break;
+    case 12: lds_wait_le<12>(); break;
+    case 13: lds_wait_le<13>(); break;
+    case 14: lds_wait_le<14>(); break;
+    default: lds_wait_le<15>(); break;
+  }
+}
+
 // 16-byte LDS read issued as inline asm (not reordered with the other asm LDS
 // reads); like lds_read_tr16 the result needs a wait and lds_ready() before use.
 __device__ __forceinline__ s16x8 lds_read_b128(const void *lds_addr) {

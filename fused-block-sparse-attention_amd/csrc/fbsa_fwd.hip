@@ -55,28 +55,6 @@ template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0> struc
 #define FBSA_FWD_KFIRST 1
 #endif
 
-// lgkmcnt wait for a count known after unrolling (values above 15 wait for 15)
-__device__ __forceinline__ void lds_wait_upto(int n) {
-  switch (n < 15 ? n : 15) {
-    case 0: lds_wait_le<0>(); break;
-    case 1: lds_wait_le<1>(); break;
-    case 2: lds_wait_le<2>(); break;
-    case 3: lds_wait_le<3>(); break;
-    case 4: lds_wait_le<4>(); break;
-    case 5: lds_wait_le<5>(); break;
-    case 6: lds_wait_le<6>(); break;
-    case 7: lds_wait_le<7>(); break;
-    case 8: lds_wait_le<8>(); break;
-    case 9: lds_wait_le<9>(); break;
-    case 10: lds_wait_le<10>(); break;
-    case 11: lds_wait_le<11>(); break;
-    case 12: lds_wait_le<12>(); break;
-    case 13: lds_wait_le<13>(); break;
-    case 14: lds_wait_le<14>(); break;
-    default: lds_wait_le<15>(); break;
-  }
-}
-
 template <int N> __device__ __forceinline__ void wait_pending(int pending_chunks) {
   // wait until at most pending_chunks * LPT DMA loads are outstanding (N = LPT)
   switch (pending_chunks) {

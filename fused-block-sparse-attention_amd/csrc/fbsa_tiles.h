@@ -35,9 +35,32 @@ template <typename T, int D> struct RowFrag {
   }
 };
 
-template <typename T, int D, int NM>
+// W > 0 (16-bit types): the tile reads are issued as asm in a sliding window of
+// W outstanding reads, each MFMA waiting only for its own (LDS reads complete
+// in order); W = 0 leaves the schedule to the compiler.
+template <typename T, int D, int NM, int W = 0>
 __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
+  if constexpr (sizeof(T) == 2 && W > 0) {
+    constexpr int KS = D / 32, NK = NM * KS;
+    s16x8 x[NK];
+    auto rd = [&](int k) {
+      const int row = 16 * (k / KS) + p;
+      x[k] = lds_read_b128(tile + (row * CPR + ((4 * (k % KS) + g) ^ swz(row, CPR))) * 16);
+    };
+#pragma unroll
+    for (int k = 0; k < (W < NK ? W : NK); ++k) rd(k);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int last = k + W - 1 < NK - 1 ? k + W - 1 : NK - 1;  // last read issued so far
+      lds_wait_upto(last - k);
+      lds_ready(x[k]);
+      if (k % KS == 0) acc[k / KS] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc[k / KS] = Mfma16<T>::run(x[k], fr.h[k % KS], acc[k / KS]);
+      if (k + W < NK) rd(k + W);
+    }
+    return;
+  }
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
     acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
