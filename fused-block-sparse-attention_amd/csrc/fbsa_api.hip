@@ -144,7 +144,7 @@ int fbsa_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float
   return run_block_mass(d, q, k, mass, (float *)ws, (hipStream_t)stream);
 }
 
-int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, void *stream) {
+static int check_pool(const fbsa_pool_desc *d, const void *x, const void *out, const void *out2) {
   if (!d) return fail(FBSA_EINVAL, "fbsa_pool: null descriptor");
   if (d->dtype < FBSA_F32 || d->dtype > FBSA_F16) return fail(FBSA_EINVAL, "fbsa_pool: bad dtype %d", d->dtype);
   if (d->op < FBSA_POOL_MEAN_TOK_THEN_GRP || d->op > FBSA_POOL_MINMAX) return fail(FBSA_EINVAL, "fbsa_pool: bad op %d", d->op);
@@ -161,7 +161,12 @@ int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, voi
   for (int k = 0; k < 3; ++k)
     if (d->sx[k] < 0 || (d->sx[k] * es) % 16) return fail(FBSA_EINVAL, "fbsa_pool: stride[%d] must be a non-negative multiple of 16 bytes", k);
   if (d->B * (d->H / d->grp) * d->nblk > 0x7fffffffLL) return fail(FBSA_EUNSUPPORTED, "fbsa_pool: grid too large");
-  return run_pool(d, x, out, out2, (hipStream_t)stream);
+  return FBSA_OK;
+}
+
+int fbsa_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, void *stream) {
+  const int e = check_pool(d, x, out, out2);
+  return e ? e : run_pool(d, x, out, out2, (hipStream_t)stream);
 }
 
 size_t fbsa_select_workspace_bytes(const fbsa_select_desc *d) { return d ? select_workspace_bytes(d) : 0; }
@@ -226,6 +231,28 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
   void *ws = (workspace && workspace_bytes >= need && need > 0) ? workspace : nullptr;
   if (ws && !aligned(ws, 16)) return fail(FBSA_EINVAL, "fbsa_select: workspace must be 16-byte aligned");
   return run_select(d, row_begin, row_end, a, b1, b2, sel, sel_score, ws, (hipStream_t)stream);
+}
+
+int fbsa_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk,
+                            const void *k, void *kp, const fbsa_select_desc *d, int32_t *sel, float *sel_score,
+                            void *workspace, size_t workspace_bytes, void *stream) {
+  int e = check_pool(dq, q, qp, nullptr);
+  if (!e) e = check_pool(dk, k, kp, nullptr);
+  if (e) return e;
+  if (dq->op != FBSA_POOL_MEAN_TOK_THEN_GRP || dk->op != FBSA_POOL_MEAN_TOK_THEN_GRP)
+    return fail(FBSA_EINVAL, "fbsa_select_mean_pooled: both pools must be MEAN_TOK_THEN_GRP");
+  if (!d) return fail(FBSA_EINVAL, "fbsa_select_mean_pooled: null select descriptor");
+  if (d->score != FBSA_SCORE_DOT) return fail(FBSA_EINVAL, "fbsa_select_mean_pooled: score must be DOT");
+  if (dq->dtype != dk->dtype || dq->dtype != d->dtype || dq->B != dk->B || dq->B != d->B || dq->L != dk->L ||
+      dq->D != dk->D || dq->D != d->D || dq->bs != dk->bs || dq->nblk != dk->nblk || dq->nblk != d->nblk ||
+      dq->l_valid != dk->l_valid || dq->H / dq->grp != d->H || dk->H / dk->grp != d->H)
+    return fail(FBSA_EINVAL, "fbsa_select_mean_pooled: pool and select descriptors disagree");
+  e = check_select(d, 0, d->nblk, qp, kp, nullptr, sel, sel_score);
+  if (e) return e;
+  const size_t need = select_workspace_bytes(d);
+  void *ws = (workspace && workspace_bytes >= need && need > 0) ? workspace : nullptr;
+  if (ws && !aligned(ws, 16)) return fail(FBSA_EINVAL, "fbsa_select_mean_pooled: workspace must be 16-byte aligned");
+  return run_select_mean_pooled(dq, q, qp, dk, k, kp, d, sel, sel_score, ws, (hipStream_t)stream);
 }
 
 size_t fbsa_select_qmax_workspace_bytes(const fbsa_qmax_desc *d) { return d ? select_qmax_workspace_bytes(d) : 0; }

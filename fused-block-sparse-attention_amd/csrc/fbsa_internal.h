@@ -31,6 +31,8 @@ constexpr int64_t kSelWideMax = 4096;
 
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
+int run_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk, const void *k,
+                           void *kp, const fbsa_select_desc *d, int32_t *sel, float *sel_score, void *ws, hipStream_t s);
 int run_block_mass(const fbsa_attn_desc *d, const void *q, const void *k, float *mass, float *lse, hipStream_t s);
 size_t select_workspace_bytes(const fbsa_select_desc *d);
 int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *a, const void *b1, const void *b2,

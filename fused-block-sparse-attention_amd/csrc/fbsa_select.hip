@@ -38,7 +38,37 @@ struct PoolArgs {
   int64_t B, H, L, D, bs, nblk, grp, l_valid, Ho;
   int64_t sx[3];
   int op;
+  // optional (mean ops of pool_wave_kernel): the selection's row norm of every
+  // pooled row, at norm[(b * Ho + ho) * norm_pitch + block]; norm_key: rounded
+  // up to bf16 (candidate side) instead of fp32 (query side)
+  float *norm;
+  int64_t norm_pitch;
+  int norm_key;
 };
+
+// bf16 bit pattern of the smallest bf16 value >= x (x >= 0, +inf or NaN).
+__device__ __forceinline__ uint32_t bf16_up_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u & 0xFFFFu) u = (u + 0x10000u) & 0xFFFF0000u;
+  return u >> 16;
+}
+
+// Row norm for the bracketed MFMA selection from an exact sum of squares:
+// rounded up (a bound must not shrink); norms outside [2^-40, 1e18] become
+// +inf, so every pair they touch has no usable bound (inf or NaN) and takes the
+// exact path, which keeps the MFMA accumulation away from fp32 overflow and
+// underflow. Candidate-side norms are rounded up to bf16, the precision of the
+// rank-1 MFMA term.
+__device__ __forceinline__ float sel_row_norm(double ss, bool key) {
+  float n;
+  if (ss == 0.0) {
+    n = 0.f;
+  } else {
+    const double nrm = sqrt(ss) * (1.0 + 1e-6);
+    n = nrm >= 0x1p-40 && nrm <= 1e18 ? (float)nrm : INFINITY;
+  }
+  return key ? __uint_as_float(bf16_up_bits(n) << 16) : n;
+}
 
 // Raw 8-element row chunk (kept undecoded until used, to keep registers low).
 template <typename T> struct Raw8 {
@@ -216,14 +246,17 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
 // are issued back to back (fixed trip count; rows past l_valid are read at a
 // clamped address and contribute 0). MEAN_TOK_THEN_GRP gives each wave whole
 // heads; the other ops split the block's tokens over the waves.
+// Workgroups [0, nwg0) pool a0, the rest pool a1 (two tensors in one launch).
 template <typename T, int DC, int BS, int OP>
-__global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
+__global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a0, PoolArgs a1, int64_t nwg0) {
   constexpr int NW = 4, TLW = 64 / DC;
   constexpr int RPH = BS >= TLW ? BS / TLW : 1;            // rows per lane per head (whole block in one wave)
   constexpr int RPW = BS >= NW * TLW ? BS / (NW * TLW) : 1;  // rows per lane when the waves split the block
   __shared__ double red[2][NW][DC][8];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane % DC, tl = lane / DC;
-  const int64_t blk = blockIdx.x;
+  const bool second = (int64_t)blockIdx.x >= nwg0;
+  const PoolArgs a = second ? a1 : a0;
+  const int64_t blk = second ? (int64_t)blockIdx.x - nwg0 : (int64_t)blockIdx.x;
   const int64_t i = blk % a.nblk;
   const int64_t ho = (blk / a.nblk) % a.Ho;
   const int64_t b = blk / (a.nblk * a.Ho);
@@ -331,7 +364,9 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
       double tot = 0.0;
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww) tot += red[0][ww][cc][e];
-      ((T *)a.out)[off] = (T)round_dt<T>(mean_div(tot, op == FBSA_POOL_MEAN_TOK_THEN_GRP ? a.grp : (int64_t)BS));
+      const T y = (T)round_dt<T>(mean_div(tot, op == FBSA_POOL_MEAN_TOK_THEN_GRP ? a.grp : (int64_t)BS));
+      ((T *)a.out)[off] = y;
+      red[1][0][cc][e] = (double)(float)y;  // element 8 cc + e of the pooled row (red[1] is free here)
     } else {
       double mn = red[0][0][cc][e], mx = red[1][0][cc][e];
 #pragma unroll
@@ -339,6 +374,19 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a) {
       if (a.op == FBSA_POOL_MAX) ((T *)a.out)[off] = (T)(float)mx;
       else if (a.op == FBSA_POOL_MIN) ((T *)a.out)[off] = (T)(float)mn;
       else { ((T *)a.out)[off] = (T)(float)mn; ((T *)a.out2)[off] = (T)(float)mx; }
+    }
+  }
+  if constexpr (op == FBSA_POOL_MEAN_TOK_THEN_GRP || op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
+    if (a.norm) {
+      // the pooled row's sum of squares over d = 0, 1, ... in order (the sum
+      // sel_norms_kernel forms from the stored row)
+      __syncthreads();
+      if (tid == 0) {
+        const double *row = &red[1][0][0][0];
+        double ss = 0.0;
+        for (int d = 0; d < DC * 8; ++d) ss += row[d] * row[d];
+        a.norm[(b * a.Ho + ho) * a.norm_pitch + i] = sel_row_norm(ss, a.norm_key != 0);
+      }
     }
   }
 }
@@ -394,13 +442,15 @@ __global__ __launch_bounds__(256) void pool_grp_kernel(PoolArgs a, int64_t n) {
 template <typename T, int DC, int BS> static void launch_pool_op(const PoolArgs &a, int64_t nwg, hipStream_t s) {
   switch (a.op) {
     case FBSA_POOL_MEAN_TOK_THEN_GRP:
-      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_TOK_THEN_GRP>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_TOK_THEN_GRP>), dim3((unsigned)nwg), dim3(256), 0, s, a,
+                         a, nwg);
       return;
     case FBSA_POOL_MEAN_GRP_THEN_TOK:
-      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_GRP_THEN_TOK>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_GRP_THEN_TOK>), dim3((unsigned)nwg), dim3(256), 0, s, a,
+                         a, nwg);
       return;
     default:  // MAX / MIN / MINMAX share one instantiation (the op picks the outputs)
-      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MINMAX>), dim3((unsigned)nwg), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MINMAX>), dim3((unsigned)nwg), dim3(256), 0, s, a, a, nwg);
       return;
   }
 }
@@ -427,12 +477,18 @@ template <typename T> static void launch_pool(const PoolArgs &a, int64_t nwg, hi
   if (!done) hipLaunchKernelGGL(pool_kernel<T>, dim3((unsigned)nwg), dim3(256), 0, s, a);
 }
 
-int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s) {
+static PoolArgs pool_args(const fbsa_pool_desc *d, const void *x, void *out, void *out2) {
   PoolArgs a;
   a.x = x; a.out = out; a.out2 = out2;
   a.B = d->B; a.H = d->H; a.L = d->L; a.D = d->D; a.bs = d->bs; a.nblk = d->nblk; a.grp = d->grp;
   a.l_valid = d->l_valid; a.Ho = d->H / d->grp; a.op = d->op;
   for (int k = 0; k < 3; ++k) a.sx[k] = d->sx[k];
+  a.norm = nullptr; a.norm_pitch = 0; a.norm_key = 0;
+  return a;
+}
+
+int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s) {
+  const PoolArgs a = pool_args(d, x, out, out2);
   const int64_t nwg = a.B * a.Ho * a.nblk;
   if (a.bs == 1 && a.op == FBSA_POOL_MEAN_GRP_THEN_TOK) {
     const int64_t n = nwg * (a.D / 8);
@@ -458,6 +514,7 @@ struct SelArgs {
   int32_t *sel;
   float *sel_score;
   const float *an1, *an2, *bn1, *bn2;  // row norms (MFMA path): query-side parts and key-side operands
+  int norms_ready;                      // the workspace's norm arrays are already filled (by the pooling)
   uint64_t *part;                      // MFMA path: per-(row, candidate chunk) top-k keys
   int64_t B, H, nblk, D, topk, kk;
   int64_t ct, nch;                     // MFMA path: candidate tiles per chunk, chunks per row block
@@ -797,12 +854,6 @@ __global__ __launch_bounds__(256) void select_wide_kernel(SelArgs a, int KP) {
 // two-stage direct-to-LDS ring shared by the waves. Rows with more than one
 // chunk leave per-chunk top-k keys that select_merge_kernel combines.
 
-// bf16 bit pattern of the smallest bf16 value >= x (x >= 0, +inf or NaN).
-__device__ __forceinline__ uint32_t bf16_up_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if (u & 0xFFFFu) u = (u + 0x10000u) & 0xFFFF0000u;
-  return u >> 16;
-}
 // max(m, x) ignoring a NaN x (IEEE maxNum); one instruction.
 __device__ __forceinline__ float vmax(float m, float x) {
   float r;
@@ -843,20 +894,10 @@ __global__ __launch_bounds__(256) void sel_norms_kernel(SelArgs a, int64_t nneed
       if (MODE != FBSA_SCORE_DOT) sb2 += w2[e] * w2[e];
     }
   }
-  // Norms rounded up (the bounds must not shrink). Norms outside
-  // [2^-40, 1e18] become +inf: every pair they touch then has no usable
-  // bound (inf or NaN) and reaches the exact path; this keeps the MFMA
-  // accumulation away from fp32 overflow and underflow. Key-side norms are
-  // stored rounded up to bf16, the precision of the rank-1 MFMA term.
-  auto sane = [](double ss) -> float {
-    if (ss == 0.0) return 0.f;
-    const double nrm = sqrt(ss) * (1.0 + 1e-6);
-    return nrm >= 0x1p-40 && nrm <= 1e18 ? (float)nrm : INFINITY;
-  };
-  an1[nrow] = sane(sa1);
-  an2[nrow] = sane(sa2);
-  bn1[nrow] = __uint_as_float(bf16_up_bits(sane(sb1)) << 16);
-  bn2[nrow] = __uint_as_float(bf16_up_bits(sane(sb2)) << 16);
+  an1[nrow] = sel_row_norm(sa1, false);
+  an2[nrow] = sel_row_norm(sa2, false);
+  bn1[nrow] = sel_row_norm(sb1, true);
+  bn2[nrow] = sel_row_norm(sb2, true);
 }
 
 // Wave-wide bitonic sort of 64 keys (one per lane), descending.
@@ -1650,10 +1691,13 @@ template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, v
       const int64_t n = a.B * a.H * nneed;
       const int64_t npad = a.B * a.H * sel_norm_pitch(a.nblk);
       float *an1 = (float *)ws, *an2 = an1 + npad, *bn1 = an2 + npad, *bn2 = bn1 + npad;
-      hipLaunchKernelGGL((sel_norms_kernel<T, D, MODE>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a,
-                         nneed, an1, an2, bn1, bn2);
-      int e = hip_check(hipGetLastError(), "sel_norms_kernel launch");
-      if (e) return e;
+      int e = FBSA_OK;
+      if (!a.norms_ready) {
+        hipLaunchKernelGGL((sel_norms_kernel<T, D, MODE>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a,
+                           nneed, an1, an2, bn1, bn2);
+        e = hip_check(hipGetLastError(), "sel_norms_kernel launch");
+        if (e) return e;
+      }
       SelArgs b = a;
       b.an1 = an1; b.an2 = an2; b.bn1 = bn1; b.bn2 = bn2;
       b.part = (uint64_t *)(((uintptr_t)(bn2 + npad) + 255) & ~(uintptr_t)255);
@@ -1723,11 +1767,12 @@ size_t select_workspace_bytes(const fbsa_select_desc *d) {
          (size_t)(n * nch * (K > 0 ? K : 1)) * sizeof(uint64_t);
 }
 
-int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *av, const void *b1, const void *b2,
-               int32_t *sel, float *sel_score, void *ws, hipStream_t s) {
+static int run_select_as(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *av, const void *b1,
+                         const void *b2, int32_t *sel, float *sel_score, void *ws, int norms_ready, hipStream_t s) {
   SelArgs a;
   a.a = av; a.b1 = b1; a.b2 = b2; a.sel = sel; a.sel_score = sel_score;
   a.an1 = a.an2 = a.bn1 = a.bn2 = nullptr;
+  a.norms_ready = norms_ready;
   a.part = nullptr;
   a.row0 = row0;
   a.row1 = row1;
@@ -1740,6 +1785,56 @@ int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void
     case FBSA_F16: return sel_d<f16>(a, ws, s);
     default: return sel_d<float>(a, ws, s);
   }
+}
+
+int run_select(const fbsa_select_desc *d, int64_t row0, int64_t row1, const void *av, const void *b1, const void *b2,
+               int32_t *sel, float *sel_score, void *ws, hipStream_t s) {
+  return run_select_as(d, row0, row1, av, b1, b2, sel, sel_score, ws, 0, s);
+}
+
+// Mean-pooled q.k selection. With the MFMA engine's workspace, 16-bit
+// operands of dim 32 or 64 and a budget of at most 48, q and k are pooled by
+// one launch that also writes the selection's row norms (query side into the
+// first norm array, candidate side into the third; DOT scores use no others),
+// and the selection starts from them; otherwise pool, pool and select run as
+// three calls. Either way qp, kp and sel are the same.
+template <typename T, int D> static int pooled_pair(const fbsa_pool_desc *dq, const void *q, void *qp,
+                                                    const fbsa_pool_desc *dk, const void *k, void *kp,
+                                                    const fbsa_select_desc *d, float *nq, float *nk, hipStream_t s) {
+  constexpr int DC = D / 8;
+  PoolArgs a0 = pool_args(dq, q, qp, nullptr), a1 = pool_args(dk, k, kp, nullptr);
+  const int64_t pitch = sel_norm_pitch(d->nblk);
+  a0.norm = nq; a0.norm_pitch = pitch; a0.norm_key = 0;
+  a1.norm = nk; a1.norm_pitch = pitch; a1.norm_key = 1;
+  const int64_t nwg0 = a0.B * a0.Ho * a0.nblk, nwg1 = a1.B * a1.Ho * a1.nblk;
+  const dim3 grid((unsigned)(nwg0 + nwg1));
+  switch (dq->bs) {
+    case 16: hipLaunchKernelGGL((pool_wave_kernel<T, DC, 16, FBSA_POOL_MEAN_TOK_THEN_GRP>), grid, dim3(256), 0, s, a0, a1, nwg0); break;
+    case 32: hipLaunchKernelGGL((pool_wave_kernel<T, DC, 32, FBSA_POOL_MEAN_TOK_THEN_GRP>), grid, dim3(256), 0, s, a0, a1, nwg0); break;
+    case 64: hipLaunchKernelGGL((pool_wave_kernel<T, DC, 64, FBSA_POOL_MEAN_TOK_THEN_GRP>), grid, dim3(256), 0, s, a0, a1, nwg0); break;
+    default: hipLaunchKernelGGL((pool_wave_kernel<T, DC, 128, FBSA_POOL_MEAN_TOK_THEN_GRP>), grid, dim3(256), 0, s, a0, a1, nwg0); break;
+  }
+  return hip_check(hipGetLastError(), "pool_wave_kernel (pair) launch");
+}
+
+int run_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk, const void *k,
+                           void *kp, const fbsa_select_desc *d, int32_t *sel, float *sel_score, void *ws, hipStream_t s) {
+  const int64_t K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1;
+  const bool fused = ws && d->dtype != FBSA_F32 && (d->D == 32 || d->D == 64) && K >= 1 && K <= 48 &&
+                     (dq->bs == 16 || dq->bs == 32 || dq->bs == 64 || dq->bs == 128);
+  if (!fused) {
+    int e = run_pool(dq, q, qp, nullptr, s);
+    if (!e) e = run_pool(dk, k, kp, nullptr, s);
+    return e ? e : run_select(d, 0, d->nblk, qp, kp, nullptr, sel, sel_score, ws, s);
+  }
+  const int64_t npad = d->B * d->H * sel_norm_pitch(d->nblk);
+  float *nq = (float *)ws, *nk = nq + 2 * npad;
+  int e;
+  if (d->dtype == FBSA_BF16) e = d->D == 32 ? pooled_pair<bf16, 32>(dq, q, qp, dk, k, kp, d, nq, nk, s)
+                                            : pooled_pair<bf16, 64>(dq, q, qp, dk, k, kp, d, nq, nk, s);
+  else e = d->D == 32 ? pooled_pair<f16, 32>(dq, q, qp, dk, k, kp, d, nq, nk, s)
+                      : pooled_pair<f16, 64>(dq, q, qp, dk, k, kp, d, nq, nk, s);
+  return e ? e : run_select_as(d, 0, d->nblk, qp, kp, nullptr, sel, sel_score, ws, 1, s);
 }
 
 }  // namespace fbsa

@@ -87,6 +87,8 @@ SIGNATURES = {
     "fbsa_select_rows": (ctypes.c_int, [ctypes.POINTER(SelectDesc), ctypes.c_int64, ctypes.c_int64,
                                         _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "fbsa_select_noalloc": (ctypes.c_int, [ctypes.POINTER(SelectDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fbsa_select_mean_pooled": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _vp, _vp, ctypes.POINTER(PoolDesc), _vp, _vp,
+                                               ctypes.POINTER(SelectDesc), _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "fbsa_select_qmax_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(QmaxDesc)]),
     "fbsa_select_qmax": (ctypes.c_int, [ctypes.POINTER(QmaxDesc), _vp, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_size_t, _vp]),

@@ -18,6 +18,23 @@ SCORES = {"dot": _lib.SCORE_DOT, "max2": _lib.SCORE_MAX2, "quest": _lib.SCORE_QU
 MAX_TOPK = 4096  # largest top-k budget of fbsa_select (past 62: one workgroup per row, keys in LDS)
 
 
+def _pool_desc(x, bs, op, grp, l_valid):
+    B, H, L, D = x.shape
+    d = _lib.PoolDesc()
+    d.dtype = _dtype_code(x)
+    d.op = POOL_OPS[op]
+    d.B, d.H, d.L, d.D, d.bs, d.nblk, d.grp = B, H, L, D, bs, (L + bs - 1) // bs, grp
+    d.l_valid = L if l_valid is None else int(l_valid)
+    d.sx[:] = (x.stride(0), x.stride(1), x.stride(2))
+    return d
+
+
+def _pool_input(x):
+    if x.stride(-1) != 1 or any((s * x.element_size()) % 16 for s in x.stride()[:-1]) or x.data_ptr() % 16:
+        return x.contiguous()
+    return x
+
+
 def pool(x, bs, op, grp=1, l_valid=None):
     """Pool x (B,H,L,D) over blocks of bs tokens (and groups of grp heads).
 
@@ -31,15 +48,9 @@ def pool(x, bs, op, grp=1, l_valid=None):
     if x.dim() != 4:
         raise ValueError("fbsa.pool: x must be (B, H, L, D)")
     B, H, L, D = x.shape
-    if x.stride(-1) != 1 or any((s * x.element_size()) % 16 for s in x.stride()[:-1]) or x.data_ptr() % 16:
-        x = x.contiguous()
+    x = _pool_input(x)
     nblk = (L + bs - 1) // bs
-    d = _lib.PoolDesc()
-    d.dtype = _dtype_code(x)
-    d.op = POOL_OPS[op]
-    d.B, d.H, d.L, d.D, d.bs, d.nblk, d.grp = B, H, L, D, bs, nblk, grp
-    d.l_valid = L if l_valid is None else int(l_valid)
-    d.sx[:] = (x.stride(0), x.stride(1), x.stride(2))
+    d = _pool_desc(x, bs, op, grp, l_valid)
     out = torch.empty(B, H // grp if H % grp == 0 else 1, nblk, D, dtype=x.dtype, device=x.device)
     out2 = torch.empty_like(out) if op == "minmax" else None
     _lib.check(_lib.load().fbsa_pool(d, _ptr(x), _ptr(out), _ptr(out2), _stream()), "fbsa_pool")
@@ -127,14 +138,42 @@ def select_mean_pooled(q, k, bs, topk, causal=True, need_scores=False, engine="a
     raw = qpool kpool^T (src/scale_sel.py:33), then own block + top-k content
     blocks (src/ssa_model.py:151-165). Returns sel (B, nblk, kk) int32.
     """
-    H = q.shape[1]
-    qp = pool(q, bs, "mean_tok_then_grp", grp=H)
-    kp = pool(k, bs, "mean_tok_then_grp", grp=k.shape[1])
-    out = select(qp, kp, score="dot", convention="own_first", topk=topk, causal=causal, need_scores=need_scores,
-                 engine=engine)
+    if engine == "fp64" or q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:] \
+            or q.dtype != k.dtype:
+        H = q.shape[1]
+        qp = pool(q, bs, "mean_tok_then_grp", grp=H)
+        kp = pool(k, bs, "mean_tok_then_grp", grp=k.shape[1])
+        out = select(qp, kp, score="dot", convention="own_first", topk=topk, causal=causal, need_scores=need_scores,
+                     engine=engine)
+        if need_scores:
+            return out[0][:, 0], out[1][:, 0]
+        return out[:, 0]
+    # one call: q and k pooled by one launch that also writes the selection's
+    # row norms (fbsa_select_mean_pooled), then the MFMA selection
+    _require_cuda(q, k)
+    q, k = _pool_input(q), _pool_input(k)
+    B, H, L, D = q.shape
+    nblk = (L + bs - 1) // bs
+    dq = _pool_desc(q, bs, "mean_tok_then_grp", H, None)
+    dk = _pool_desc(k, bs, "mean_tok_then_grp", k.shape[1], None)
+    kk = budget("own_first", topk, nblk)
+    d = _lib.SelectDesc()
+    d.dtype = _dtype_code(q)
+    d.score, d.convention = _lib.SCORE_DOT, _lib.SEL_OWN_FIRST
+    d.causal, d.sink, d.flags = 1 if causal else 0, 0, 0
+    d.B, d.H, d.nblk, d.D, d.topk, d.kk = B, 1, nblk, D, topk, kk
+    qp = torch.empty(B, 1, nblk, D, dtype=q.dtype, device=q.device)
+    kp = torch.empty_like(qp)
+    sel = torch.empty(B, 1, nblk, kk, dtype=torch.int32, device=q.device)
+    sc = torch.empty(B, 1, nblk, kk, dtype=torch.float32, device=q.device) if need_scores else None
+    lib = _lib.load()
+    nbytes = lib.fbsa_select_workspace_bytes(d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    _lib.check(lib.fbsa_select_mean_pooled(dq, _ptr(q), _ptr(qp), dk, _ptr(k), _ptr(kp), d, _ptr(sel), _ptr(sc),
+                                           _ptr(ws), nbytes, _stream()), "fbsa_select_mean_pooled")
     if need_scores:
-        return out[0][:, 0], out[1][:, 0]
-    return out[:, 0]
+        return sel[:, 0], sc[:, 0]
+    return sel[:, 0]
 
 
 def select_quest(q, k, bs, topk, sink=True, l_valid=None, engine="auto"):

@@ -174,6 +174,22 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
                      const void *b1, const void *b2, int32_t *sel, float *sel_score, void *workspace,
                      size_t workspace_bytes, void *stream);
 
+/* Mean-pooled q.k block selection in one call: pools q into qp and k into kp
+ * (dq, dk: op MEAN_TOK_THEN_GRP; outputs (B, H/grp, nblk, D) contiguous, as
+ * fbsa_pool writes them) and selects with score DOT over (qp, kp) as
+ * fbsa_select with d. dq and dk share dtype, B, L, D, bs, nblk and l_valid,
+ * and H/grp equals d->H for both. With a workspace of at least
+ * fbsa_select_workspace_bytes(d) bytes and 16-bit operands of dim 32 or 64
+ * (top-k budget <= 48), both tensors are pooled by one launch that also writes
+ * the selection's row norms, so the call takes three launches instead of five;
+ * otherwise it runs fbsa_pool twice and fbsa_select. qp, kp, sel and sel_score
+ * are identical either way. Replaces the pooling of src/ssa_model.py:287-288
+ * (and src/bench_crossover.py:41-45), the score qpool.kpool^T of
+ * src/scale_sel.py:33 and the top-k of src/ssa_model.py:151-165. */
+int fbsa_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk,
+                            const void *k, void *kp, const fbsa_select_desc *d, int32_t *sel,
+                            float *sel_score, void *workspace, size_t workspace_bytes, void *stream);
+
 /* fbsa_select without a workspace argument and without any allocation, for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the

@@ -116,6 +116,40 @@ def test_select_flags_and_workspace_size():
     assert lib.fbsa_select_workspace_bytes(d) == 0
 
 
+def test_select_mean_pooled_validates_descriptors():
+    lib = _lib.load()
+
+    def pdesc(H):
+        d = _lib.PoolDesc()
+        d.dtype, d.op = _lib.BF16, _lib.POOL_MEAN_TOK_THEN_GRP
+        d.B, d.H, d.L, d.D, d.bs, d.nblk, d.grp, d.l_valid = 1, H, 4096, 64, 64, 64, H, 4096
+        d.sx[:] = (H * 4096 * 64, 4096 * 64, 64)
+        return d
+    dq, dk = pdesc(8), pdesc(2)
+    s = _lib.SelectDesc()
+    s.dtype, s.score, s.convention, s.causal = _lib.BF16, _lib.SCORE_DOT, _lib.SEL_OWN_FIRST, 1
+    s.B, s.H, s.nblk, s.D, s.topk, s.kk = 1, 1, 64, 64, 16, 17
+
+    def call():
+        return lib.fbsa_select_mean_pooled(dq, DUMMY, DUMMY, dk, DUMMY, DUMMY, s, DUMMY, None, None, 0, None)
+    dq.op = _lib.POOL_MEAN_GRP_THEN_TOK
+    assert call() == _lib.EINVAL and "MEAN_TOK_THEN_GRP" in lib.fbsa_last_error().decode()
+    dq.op = _lib.POOL_MEAN_TOK_THEN_GRP
+    s.score = _lib.SCORE_MAX2
+    assert call() == _lib.EINVAL and "DOT" in lib.fbsa_last_error().decode()
+    s.score = _lib.SCORE_DOT
+    for field, bad in (("H", 2), ("nblk", 32), ("D", 32)):
+        good = getattr(s, field)
+        setattr(s, field, bad)
+        assert call() == _lib.EINVAL and "disagree" in lib.fbsa_last_error().decode(), field
+        setattr(s, field, good)
+    dk.l_valid = 4000
+    assert call() == _lib.EINVAL and "disagree" in lib.fbsa_last_error().decode()
+    dk.l_valid = 4096
+    s.kk = 16
+    assert call() == _lib.EINVAL and "kk" in lib.fbsa_last_error().decode()
+
+
 def test_row_range_entry_points_validate_ranges():
     lib = _lib.load()
     d = _lib.SelectDesc()

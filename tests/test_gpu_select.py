@@ -74,6 +74,35 @@ def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal, engine):
     assert np.array_equal(sc.cpu().numpy().astype(np.float64), ref_sc)
 
 
+@pytest.mark.parametrize("dtype,B,Hq,Hk,N,D,bs,topk,scale", [
+    ("bf16", 1, 8, 8, 16384, 64, 64, 16, 1.0),     # config 3's shape, shorter
+    ("bf16", 2, 4, 2, 3000, 64, 32, 48, 1.0),      # ragged tail block, largest fused budget
+    ("f16", 1, 2, 1, 2048, 32, 16, 8, 1.0),
+    ("bf16", 1, 2, 2, 4096, 64, 128, 20, 1.0),
+    ("bf16", 1, 4, 4, 4096, 64, 64, 49, 1.0),      # budget past the MFMA engine: pool, pool, select
+    ("bf16", 1, 2, 2, 4096, 64, 64, 16, 1e19),     # norms past 1e18: every pair takes the exact path
+    ("bf16", 1, 2, 2, 4096, 32, 64, 16, 1e-20),    # norms below 2^-40: likewise
+])
+def test_select_mean_pooled_fused_equals_separate_calls(dtype, B, Hq, Hk, N, D, bs, topk, scale):
+    """fbsa_select_mean_pooled (q and k pooled by one launch that also writes the
+    selection's row norms) against fbsa_pool twice + fbsa_select: same blocks,
+    same chosen-slot scores."""
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(31)
+    q = (randn(g, (B, Hq, N, D), "f32") * scale).to(getattr(torch, {"bf16": "bfloat16", "f16": "float16"}[dtype]))
+    k = (randn(g, (B, Hk, N, D), "f32") * scale).to(q.dtype)
+    q, k = q.to(DEV), k.to(DEV)
+    _say("mean-pooled fused vs separate", dtype, B, Hq, Hk, N, D, bs, topk, scale)
+    sel1, sc1 = selection.select_mean_pooled(q, k, bs, topk, True, need_scores=True)
+    qp = selection.pool(q, bs, "mean_tok_then_grp", grp=Hq)
+    kp = selection.pool(k, bs, "mean_tok_then_grp", grp=Hk)
+    sel2, sc2 = selection.select(qp, kp, score="dot", convention="own_first", topk=topk, causal=True,
+                                 need_scores=True)
+    torch.cuda.synchronize()
+    assert torch.equal(sel1, sel2[:, 0])
+    assert torch.equal(sc1, sc2[:, 0])
+
+
 def test_select_config3_full_size_sampled_rows():
     # config 3: B1 H8 N262144 D64 bs64 top-16; q,k ~ N(0,1)/8 in bf16. The oracle
     # pools the full tensors and scores a sample of rows (each row i depends
