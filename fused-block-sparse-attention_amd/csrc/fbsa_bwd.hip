@@ -53,6 +53,11 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #define FBSA_DKDV_WIN 8
 #endif
 
+// extra list segments: a segment's workgroups placed on one XCD
+#ifndef FBSA_XSEG_XCD
+#define FBSA_XSEG_XCD 1
+#endif
+
 // work chunks (KC query rows of one reading query block and head) per dK/dV list segment
 #ifndef FBSA_SEG_CHUNKS
 #define FBSA_SEG_CHUNKS 512
@@ -647,7 +652,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
   int4 *s_meta = (int4 *)(smem + C::NSTAGE * C::STAGE_BYTES);  // per entry: query block, mask kind, gate bits
-  float4 *s_xch = (float4 *)(s_meta + MAXE);  // two roles: P of each key group's part, [KEYS/16][64 lanes][HR/16]
+  float4 *s_xch = (float4 *)(s_meta + MAXE);  // two roles: P of each key group's part, [HR/16][KEYS/16][64 lanes]
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
   // Launch order. Causal selection gives low key blocks far longer transposed
@@ -667,8 +672,10 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   int64_t t;
   const bool extra = bid < nx * NPART;
   if (extra) {
-    const int4 xe = a.xtab[bid / NPART];
-    kpart = (int)(bid % NPART);
+    // the NPART workgroups of an extra segment on one XCD too (they read the
+    // same Q / dO tiles)
+    const int4 xe = a.xtab[FBSA_XSEG_XCD ? gqa_unit(bid, nx, NPART, &kpart) : bid / NPART];
+    if (!FBSA_XSEG_XCD) kpart = (int)(bid % NPART);
     t = xe.x; e0 = xe.y; e1 = xe.z; slot = xe.w;
   } else {
     bid -= nx * NPART;
@@ -829,7 +836,10 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         if constexpr (ROLES == 2) {
           f32x4 xacc[HR / 16];
           mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
-          float4 *xs = s_xch + (kw * 64 + lane) * (HR / 16);
+          // element m of this lane at s_xch[(m * KEYS/16 + kw) * 64 + lane]: a wave's
+          // 16-byte accesses are consecutive, on distinct banks
+          float4 *xs = s_xch + kw * 64 + lane;
+          constexpr int XS = (KEYS / 16) * 64;  // stride between the parts m
           float x[HR / 16][4];
           if (role == 0) {
 #pragma unroll
@@ -842,7 +852,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 asm volatile("" : "+v"(ev));
                 x[m][r] = ok ? ev : 0.f;
               }
-              xs[m] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
+              xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
             }
           }
           lds_barrier();  // P of this part is in LDS for the role-1 waves
@@ -851,7 +861,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
           } else {
 #pragma unroll
             for (int m = 0; m < HR / 16; ++m) {
-              const float4 pv = xs[m];
+              const float4 pv = xs[m * XS];
               const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
               for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
