@@ -630,9 +630,22 @@ template <typename T, int BS, int D> constexpr int dkdv_minwg() {
 #ifndef FBSA_DKDV_HEAVY_LDS_BUDGET
 #define FBSA_DKDV_HEAVY_LDS_BUDGET 102400
 #endif
+// Two roles, one barrier per chunk: the P hand-over of chunk c is consumed after
+// the ring barrier of chunk c + 1 (so a stage is read in two iterations and the
+// ring needs one stage more for the same prefetch depth)
+#ifndef FBSA_DKDV_PIPE
+#define FBSA_DKDV_PIPE 1
+#endif
+#ifndef FBSA_DKDV_PIPE_LDS_BUDGET
+#define FBSA_DKDV_PIPE_LDS_BUDGET 132096
+#endif
+template <typename T, int BS, int D> constexpr bool dkdv_pipe() {
+  return dkdv_roles<T, D>() == 2 && dkdv_rows<T, BS, D>() >= 128 && FBSA_DKDV_PIPE;
+}
 template <typename T, int BS, int D>
 using DkdvCfg = BwdCfg<T, BS, D,
-                       dkdv_heavy<T, D>() && (dkdv_roles<T, D>() == 2 ? dkdv_rows<T, BS, D>() >= 64
+                       dkdv_pipe<T, BS, D>() ? FBSA_DKDV_PIPE_LDS_BUDGET
+                       : dkdv_heavy<T, D>() && (dkdv_roles<T, D>() == 2 ? dkdv_rows<T, BS, D>() >= 64
                                                                      : dkdv_rows<T, BS, D>() == 64)
                            ? FBSA_DKDV_HEAVY_LDS_BUDGET / dkdv_minwg<T, BS, D>()
                            : FBSA_DKDV_LDS_BUDGET,
@@ -781,6 +794,99 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
       }
       if (++istg == C::NSTAGE) istg = 0;
     };
+    if constexpr (dkdv_pipe<T, BS, D>()) {
+      // Two roles, one barrier per chunk. Iteration c: barrier; refill the
+      // stage of chunk c - 2; finish chunk c - 1 (role 0: dV += dO^T P from
+      // its registers; role 1: P from the exchange buffer written before this
+      // barrier, dS, dK += Q^T dS); start chunk c (role 0: S, P into exchange
+      // buffer c & 1; role 1: dP kept in registers). A stage is read in two
+      // iterations, so AHEAD = NSTAGE - 2 chunks are prefetched.
+      static_assert(C::KC == HR && C::NSTAGE >= 3, "one part per chunk, three stages or more");
+      constexpr int AHEAD = C::NSTAGE - 2;
+      constexpr int XS = (KEYS / 16) * 64;  // float4 stride between the parts m of a buffer
+#pragma unroll
+      for (int c = 0; c < AHEAD; ++c)
+        if (c < nchunks) issue();
+      wait_vmcnt<0>();
+      int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
+      float x[HR / 16][4];                   // pending chunk: P (role 0) or dP (role 1)
+      const char *pQ = stages, *pD = stages;
+      const float2 *pM = (const float2 *)stages;
+      for (int c = 0; c <= nchunks; ++c) {
+        if (c < nchunks) {
+          const int ahead = nchunks - 1 - c;
+          wait_ring<C::LPT + 1>(ahead < AHEAD - 1 ? ahead : AHEAD - 1);
+        }
+        lds_barrier();
+        if (c + AHEAD < nchunks) issue();
+        if (c > 0) {
+          if (role == 0) {
+            mm_tr_acc<T, D, HR>(pD, x, dvacc, g, p);  // dV^T += dO^T P
+          } else {
+            const float4 *xs = s_xch + ((c - 1) & 1) * (HR / 16) * XS + kw * 64 + lane;
+#pragma unroll
+            for (int m = 0; m < HR / 16; ++m) {
+              const float4 pv = xs[m * XS];
+              const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] - pM[16 * m + 4 * g + r].y);
+            }
+            mm_tr_acc<T, D, HR>(pQ, x, dvacc, g, p);  // dK^T += Q^T dS
+          }
+        }
+        if (c == nchunks) break;
+
+        const char *Qs = stages + cstg * C::STAGE_BYTES;
+        const char *Ds = Qs + C::TILE_BYTES;
+        const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
+        const int4 meta = s_meta[cx];
+        const int ch = cch;
+        const int kind = meta.y;
+        const float gt = __int_as_float(meta.z);
+        const int64_t i = meta.x;
+        if (++cch == C::NCH) {
+          cch = 0;
+          if (++cg == a.grp) { cg = 0; ++cx; }
+        }
+        if (++cstg == C::NSTAGE) cstg = 0;
+        int tmin = -(1 << 30);
+        bool kok = true;
+        if (kind == KIND_DIAG) tmin = u;
+        else if (kind == KIND_PAD) kok = keyok;
+        else if (kind == KIND_ABS) {
+          const int64_t tm = (int64_t)u - (i - j) * BS;
+          tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);
+          kok = keyok;
+        }
+        tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
+
+        f32x4 xacc[HR / 16];
+        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Ds : Qs, kf, xacc, g, p);  // S or dP
+        if (role == 0) {
+          float4 *xs = s_xch + (c & 1) * (HR / 16) * XS + kw * 64 + lane;
+#pragma unroll
+          for (int m = 0; m < HR / 16; ++m) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float2 ms = Ms[16 * m + 4 * g + r];
+              const bool ok = kok && (16 * m + r >= tmin);
+              float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, gt - ms.x));
+              asm volatile("" : "+v"(ev));
+              x[m][r] = ok ? ev : 0.f;
+            }
+            xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < HR / 16; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[m][r] = xacc[m][r];
+        }
+        pQ = Qs; pD = Ds; pM = Ms;
+      }
+      continue;
+    }
+
 #pragma unroll
     for (int c = 0; c < C::NSTAGE - 1; ++c)
       if (c < nchunks) issue();
@@ -1086,7 +1192,9 @@ template <typename T, int BS, int D, bool DENSE> static int launch_dq_as(const B
 template <typename T, int BS, int D, bool DENSE> static int launch_dkdv_as(const BwdArgs &a, hipStream_t s) {
   using C = DkdvCfg<T, BS, D>;
   constexpr int HR = C::KC >= 64 ? 32 : C::KC;
-  const size_t xch = dkdv_roles<T, D>() == 2 ? (size_t)(dkdv_keys<T, BS, D>() / 16) * 64 * (HR / 16) * 16 : 0;
+  const size_t xch = dkdv_roles<T, D>() == 2
+                         ? (size_t)(dkdv_pipe<T, BS, D>() ? 2 : 1) * (dkdv_keys<T, BS, D>() / 16) * 64 * (HR / 16) * 16
+                         : 0;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16 + xch;
   static size_t granted = 0;
   int e = set_lds(dkdv_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dkdv");
