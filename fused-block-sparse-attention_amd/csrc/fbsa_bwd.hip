@@ -411,7 +411,9 @@ template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct
   static constexpr int ES = sizeof(T);
   static constexpr int NW = ROWS / 16;
   static constexpr int NT = NW * 64;
-  static constexpr int KC = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
+  // key / query rows per chunk: 64, 32 at d 256 (16-bit), 16 for fp32 at d >= 128 (registers)
+  static constexpr int KCW = ES == 4 && D >= 128 ? 16 : (D >= 256 ? 32 : 64);
+  static constexpr int KC = BS < KCW ? BS : KCW;
   static constexpr int NCH = BS / KC;
   static constexpr int CPR = D * ES / 16;
   static constexpr int TILE_BYTES = KC * D * ES;

@@ -35,7 +35,9 @@ template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0> struc
   static constexpr int ES = sizeof(T);
   static constexpr int NW = BS / (16 * QT);
   static constexpr int NT = NW * 64;
-  static constexpr int KC0 = BS < (D >= 256 ? 32 : 64) ? BS : (D >= 256 ? 32 : 64);
+  // keys per chunk: 64, 32 at d 256 (16-bit), 16 for fp32 at d >= 128 (registers)
+  static constexpr int KCW = ES == 4 && D >= 128 ? 16 : (D >= 256 ? 32 : 64);
+  static constexpr int KC0 = BS < KCW ? BS : KCW;
   static constexpr int KC = KCO ? KCO : KC0;
   static constexpr int NCH = BS / KC;
   static constexpr int CPR = D * ES / 16;
@@ -267,6 +269,8 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
           const float kf = *(const float *)(Ks + (row * C::CPR + (ks ^ swz(row, C::CPR))) * 16 + g * 4);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) sacc[qt][m] = mfma_f32_16x16x4(kf, qf32[qt][ks], sacc[qt][m]);
+          // at d 256, loads are not hoisted more than 16 MFMAs ahead (registers)
+          if constexpr (D >= 256) if (ks % 16 == 15) asm volatile("" ::: "memory");
         }
       }
     } else if constexpr (FBSA_FWD_KFIRST) {

@@ -70,7 +70,11 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
       for (int ks = 0; ks < D / 4; ++ks) {
         const float x = *(const float *)(tile + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
         acc[m] = mfma_f32_16x16x4(x, fr.f[ks], acc[m]);
+        if constexpr (D >= 256) if (ks % 16 == 15) asm volatile("" ::: "memory");  // at most 16 loads ahead
       }
+      // keeps the next row tile's loads from being hoisted above these MFMAs
+      // (at d >= 128 the hoisted loads of every tile exhaust the registers)
+      if constexpr (D >= 128) asm volatile("" ::: "memory");
     } else {
 #pragma unroll
       for (int ks = 0; ks < D / 32; ++ks) {
@@ -86,7 +90,7 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
   constexpr int CPR = D * (int)sizeof(T) / 16;
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t)
+    for (int t = 0; t < D / 16; ++t) {
 #pragma unroll
       for (int m = 0; m < KC / 16; ++m)
 #pragma unroll
@@ -95,6 +99,10 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
           const float a = *(const float *)(tile + (row * CPR + ((4 * t + (p >> 2)) ^ swz(row, CPR))) * 16 + (p & 3) * 4);
           acc[t] = mfma_f32_16x16x4(a, x[m][r], acc[t]);
         }
+      // keeps the next tile's loads from being hoisted above these MFMAs (at
+      // d >= 128 the hoisted loads of every tile exhaust the registers)
+      if constexpr (D >= 128) asm volatile("" ::: "memory");
+    }
   } else if constexpr (KC >= 32) {
     s16x8 pk[KC / 32];
 #pragma unroll
