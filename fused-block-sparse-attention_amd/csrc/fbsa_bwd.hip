@@ -52,6 +52,11 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_DKDV_WIN
 #define FBSA_DKDV_WIN 8
 #endif
+// output tiles of transposed reads in flight in the dQ / dK / dV products (d >= 128; 0 = batches of
+// 8 waited for at once)
+#ifndef FBSA_BWD_TRWIN
+#define FBSA_BWD_TRWIN 8
+#endif
 
 // extra list segments: a segment's workgroups placed on one XCD
 #ifndef FBSA_XSEG_XCD
@@ -572,7 +577,7 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
       if (lane == 0) s_dg[w * a.kk + slot] = dgl;
       dgl = 0.f;
     }
-    mm_tr_acc<T, D, C::KC>(Ks, ds, dqacc, g, p);  // dQ^T += K^T dS^T
+    mm_tr_acc<T, D, C::KC, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Ks, ds, dqacc, g, p);  // dQ^T += K^T dS^T
   }
 
   T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
@@ -823,7 +828,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         if (c + AHEAD < nchunks) issue();
         if (c > 0) {
           if (role == 0) {
-            mm_tr_acc<T, D, HR>(pD, x, dvacc, g, p);  // dV^T += dO^T P
+            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(pD, x, dvacc, g, p);  // dV^T += dO^T P
           } else {
             const float4 *xs = s_xch + ((c - 1) & 1) * (HR / 16) * XS + kw * 64 + lane;
 #pragma unroll
@@ -833,7 +838,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 #pragma unroll
               for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] - pM[16 * m + 4 * g + r].y);
             }
-            mm_tr_acc<T, D, HR>(pQ, x, dvacc, g, p);  // dK^T += Q^T dS
+            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(pQ, x, dvacc, g, p);  // dK^T += Q^T dS
           }
         }
         if (c == nchunks) break;
@@ -965,7 +970,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
           }
           lds_barrier();  // P of this part is in LDS for the role-1 waves
           if (role == 0) {
-            mm_tr_acc<T, D, HR>(Dh, x, dvacc, g, p);  // dV^T += dO^T P
+            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Dh, x, dvacc, g, p);  // dV^T += dO^T P
           } else {
 #pragma unroll
             for (int m = 0; m < HR / 16; ++m) {
@@ -974,7 +979,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 #pragma unroll
               for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
             }
-            mm_tr_acc<T, D, HR>(Qh, x, dvacc, g, p);  // dK^T += Q^T dS
+            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Qh, x, dvacc, g, p);  // dK^T += Q^T dS
           }
           continue;
         }
@@ -997,8 +1002,8 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
             pp[m][r] = pv;
             ds[m][r] = pv * (dpacc[m][r] - ms.y);
           }
-        mm_tr_acc<T, D, HR>(Dh, pp, dvacc, g, p);  // dV^T += dO^T P
-        mm_tr_acc<T, D, HR>(Qh, ds, dkacc, g, p);  // dK^T += Q^T dS
+        mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Dh, pp, dvacc, g, p);  // dV^T += dO^T P
+        mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Qh, ds, dkacc, g, p);  // dK^T += Q^T dS
       }
     }
   }

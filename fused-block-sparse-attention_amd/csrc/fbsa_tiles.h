@@ -85,9 +85,50 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
   }
 }
 
-template <typename T, int D, int KC>
+// TW > 0 (16-bit types, KC >= 32): the transposed reads go out in a sliding
+// window of TW output tiles, each tile's MFMAs waiting only for its own reads.
+template <typename T, int D, int KC, int TW = 0>
 __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC / 16][4], f32x4 *acc, int g, int p) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
+  if constexpr (sizeof(T) == 2 && KC >= 32 && TW > 0) {
+    s16x8 pk[KC / 32];
+#pragma unroll
+    for (int k2 = 0; k2 < KC / 32; ++k2) {
+      float y[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { y[r] = x[2 * k2][r]; y[4 + r] = x[2 * k2 + 1][r]; }
+      pk[k2] = pack8<T>(y);
+    }
+    constexpr int NTL = D / 16, RPT = 2 * (KC / 32);  // output tiles, reads per tile
+    constexpr int W = TW < NTL ? TW : NTL;
+    s16x4 lo[NTL][KC / 32], hi[NTL][KC / 32];
+    auto rd = [&](int t) {
+      const int cb = 2 * t + ((p & 3) >> 1);
+#pragma unroll
+      for (int k2 = 0; k2 < KC / 32; ++k2) {
+        const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
+        lo[t][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
+        hi[t][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
+      }
+    };
+#pragma unroll
+    for (int t = 0; t < W; ++t) rd(t);
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) {
+      const int last = t + W - 1 < NTL - 1 ? t + W - 1 : NTL - 1;  // last tile requested so far
+      lds_wait_upto((last - t) * RPT);
+#pragma unroll
+      for (int k2 = 0; k2 < KC / 32; ++k2) {
+        lds_ready(lo[t][k2]);
+        lds_ready(hi[t][k2]);
+        const s16x4 a = lo[t][k2], b = hi[t][k2];
+        const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        acc[t] = Mfma16<T>::run(av, pk[k2], acc[t]);
+      }
+      if (t + W < NTL) rd(t + W);
+    }
+    return;
+  }
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
