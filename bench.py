@@ -177,6 +177,61 @@ def cpu_baseline(q, k, v, bs, topk, rows_wanted):
     }
 
 
+def cpu_baseline_bwd(q, k, v, do, bs, topk, rows_wanted):
+    """The reference's backward on the host cores, in the same dtype: torch
+    autograd through the gather path of `cpu_baseline` (gathered K/V blocks,
+    additive mask, SDPA; src/ssa_model.py:57-90, 167-183), i.e. dQ for the
+    sampled query blocks and dK/dV scattered back into full-size K/V gradients.
+    One forward + backward over a bounded sample of `rows_wanted` query blocks
+    spread over the sequence; the backward alone is timed and scaled to all
+    blocks (the selection is not timed here)."""
+    import torch
+    import torch.nn.functional as F
+
+    nthreads = torch.get_num_threads()
+    qc, kc, vc, dc = (t.detach().cpu() for t in (q, k, v, do))
+    B, H, N, D = qc.shape
+    nblk = N // bs
+    rows = torch.linspace(0, nblk - 1, rows_wanted).round().long().unique()
+    NEG = torch.finfo(torch.float32).min
+    qpool = qc.view(B, H, nblk, bs, D).mean(3).mean(1)
+    kpool = kc.view(B, H, nblk, bs, D).mean(3).mean(1)
+    ar = torch.arange(nblk)
+    kk_c = min(topk, nblk - 1)
+    raw = torch.matmul(qpool[:, rows], kpool.transpose(1, 2))
+    content = raw.masked_fill(ar.view(1, 1, nblk) >= rows.view(1, -1, 1), float("-inf"))
+    sel = torch.cat([rows.view(1, -1, 1).expand(B, -1, 1), content.topk(kk_c, dim=-1).indices], dim=-1)
+    R, kk = sel.shape[1], sel.shape[2]
+    kb = kc.view(B, H, nblk, bs, D).detach().requires_grad_(True)
+    vb = vc.view(B, H, nblk, bs, D).detach().requires_grad_(True)
+    qs = qc.view(B, H, nblk, bs, D)[:, :, rows].detach().requires_grad_(True)
+    bi = torch.arange(B).view(B, 1, 1, 1)
+    hi = torch.arange(H).view(1, H, 1, 1)
+    si = sel.view(B, 1, R, kk)
+    ks = kb[bi, hi, si].reshape(B, H, R, kk * bs, D)
+    vs = vb[bi, hi, si].reshape(B, H, R, kk * bs, D)
+    tri = torch.zeros(bs, kk * bs)
+    tri[:, :bs] = torch.triu(torch.full((bs, bs), NEG), 1)
+    valid = torch.ones(B, R, kk, dtype=torch.bool)
+    valid[..., 1:] = sel[..., 1:] < rows.view(1, -1, 1)
+    blk = torch.zeros(B, R, kk).masked_fill_(~valid, NEG).repeat_interleave(bs, dim=-1).unsqueeze(2)
+    mask = (blk + tri).unsqueeze(1).to(qc.dtype)
+    o = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask)
+    g = dc.view(B, H, nblk, bs, D)[:, :, rows]
+    t0 = time.perf_counter()
+    o.backward(g)
+    t_bwd = time.perf_counter() - t0
+    scale = nblk / len(rows)
+    total = t_bwd * scale
+    return {
+        "value": B * N / total, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+        "sample": (f"torch {str(qc.dtype).replace('torch.', '')} autograd on {nthreads} host threads through "
+                   f"the reference's gather path (dQ, and dK/dV scattered into full-size gradients) for "
+                   f"{len(rows)} of {nblk} query blocks x {H} heads ({t_bwd:.2f} s), scaled x{scale:.1f} to all "
+                   f"blocks; est. {total:.1f} s per backward"),
+    }
+
+
 def rope_partial(x, dims=64, theta=1e7):
     """rotate_half rotary embedding on the first `dims` channels at positions
     0..N-1 (Qwen's partial RoPE, applied by the caller before attention)."""
@@ -426,6 +481,8 @@ def main():
 
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(q, k, v, bs, topk, a.cpu_rows)
+        if a.bwd:
+            out["bwd"]["cpu_baseline"] = cpu_baseline_bwd(q, k, v, do, bs, topk, max(1, a.cpu_rows // 16))
     print(json.dumps(out), flush=True)
 
 
