@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "fbsa.h"
 
 namespace fbsa {
@@ -163,6 +166,48 @@ __device__ __forceinline__ s16x8 lds_read_b128(const void *lds_addr) {
   return r;
 }
 template <typename V> __device__ __forceinline__ void lds_ready(V &x) { asm volatile("" : "+v"(x)); }
+// The same reads with a compile-time byte offset in the instruction's offset
+// field (vaddr = a per-lane base plus the stage address): no address VALU op
+// per read.
+template <int OFF> __device__ __forceinline__ s16x8 lds_read_b128_at(unsigned vaddr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  s16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(vaddr), "n"(OFF));
+  return r;
+}
+template <int OFF> __device__ __forceinline__ s16x4 lds_read_tr16_at(unsigned vaddr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  s16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(vaddr), "n"(OFF));
+  return r;
+}
+
+// static_for<N>(fn): fn(std::integral_constant<int, i>{}) for i = 0 .. N-1
+// (the index is a constant expression inside fn)
+template <typename Fn, int... Is>
+__device__ __forceinline__ void static_for_(Fn &&fn, std::integer_sequence<int, Is...>) {
+  (fn(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename Fn> __device__ __forceinline__ void static_for(Fn &&fn) {
+  static_for_(fn, std::make_integer_sequence<int, N>{});
+}
+
+// Swizzled operand-tile addressing as per-lane bases plus constants. swz
+// depends on row bits 0..3 only and is below 16, so for the MFMA operand read
+// of row 16m + p, chunk 4ks + g (16-bit types):
+//   byte offset = kbase(ks % 4) + (ks / 4) * 256 + m * 256 * CPR
+// with kbase(l) = (p * CPR + ((4l + g) ^ swz(p))) * 16; and for the transposing
+// read of rows ra = 32 k2 + 4g + p/4 (+16 for the high half), chunk 2t + h,
+// h = (p & 3) / 2, half p & 1:
+//   byte offset = vbase(t % 8) + (t / 8) * 256 + k2 * 512 * CPR (+ 256 * CPR)
+// with vbase(l) = ((4g + p/4) * CPR + ((2l + h) ^ swz(4g + p/4))) * 16 + (p & 1) * 8.
+__device__ __forceinline__ unsigned tile_kbase(int l, int g, int p, int cpr) {
+  return (unsigned)((p * cpr + ((4 * l + g) ^ swz(p, cpr))) * 16);
+}
+__device__ __forceinline__ unsigned tile_vbase(int l, int g, int p, int cpr) {
+  const int ra = 4 * g + (p >> 2);
+  return (unsigned)((ra * cpr + ((2 * l + ((p & 3) >> 1)) ^ swz(ra, cpr))) * 16 + (p & 1) * 8);
+}
 
 __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m, 64); }
 

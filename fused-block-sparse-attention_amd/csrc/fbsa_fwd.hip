@@ -219,6 +219,15 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   wait_vmcnt<0>();
 
 
+  // per-lane LDS bases of the operand reads (16-bit types): each read is a base
+  // plus the stage address plus a compile-time offset
+  constexpr int KL = QF < 4 ? QF : 4, VL = D / 16 < 8 ? D / 16 : 8;
+  unsigned kbl[KL], vbl[VL];
+#pragma unroll
+  for (int l = 0; l < KL; ++l) kbl[l] = tile_kbase(l, g, p, C::CPR);
+#pragma unroll
+  for (int l = 0; l < VL; ++l) vbl[l] = tile_vbase(l, g, p, C::CPR);
+
   for (int c = 0; c < nchunks; ++c) {
     // chunk c has landed once at most min(ahead, NSTAGE-2) later chunks are in flight
     const int ahead = nchunks - 1 - c;
@@ -239,19 +248,18 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
     constexpr int KV2 = C::KC >= 32 ? C::KC / 32 : 1;
     s16x4 vlo[F32 ? 1 : D / 16][KV2], vhi[F32 ? 1 : D / 16][KV2];
     auto read_v = [&]() {
-#pragma unroll
-      for (int mt = 0; mt < D / 16; ++mt) {
-        const int cb = 2 * mt + ((p & 3) >> 1);  // logical 16-B chunk of d0 = 16mt + 4(p&3)
-#pragma unroll
-        for (int k2 = 0; k2 < KV2; ++k2) {
-          const int ra = 32 * k2 + 4 * g + (p >> 2);
-          vlo[mt][k2] = lds_read_tr16(Vs + (ra * C::CPR + (cb ^ swz(ra, C::CPR))) * 16 + (p & 1) * 8);
-          if constexpr (C::KC >= 32) {
-            const int rb = ra + 16;
-            vhi[mt][k2] = lds_read_tr16(Vs + (rb * C::CPR + (cb ^ swz(rb, C::CPR))) * 16 + (p & 1) * 8);
-          }
-        }
-      }
+      // d tile mt, rows 32 k2 + 4g + p/4 (+16): lane base vbl[mt % 8] plus the
+      // stage address plus a constant
+      const unsigned vs = (unsigned)(uintptr_t)Vs;
+      static_for<(F32 ? 0 : D / 16)>([&](auto MT) {
+        constexpr int mt = decltype(MT)::value;
+        static_for<KV2>([&](auto K2) {
+          constexpr int k2 = decltype(K2)::value;
+          constexpr int off = (mt / 8) * 256 + k2 * 512 * C::CPR;
+          vlo[mt][k2] = lds_read_tr16_at<off>(vs + vbl[mt % 8]);
+          if constexpr (C::KC >= 32) vhi[mt][k2] = lds_read_tr16_at<off + 256 * C::CPR>(vs + vbl[mt % 8]);
+        });
+      });
     };
 
     // S^T (KC keys x 16 queries per tile); each K fragment feeds every tile
@@ -279,13 +287,11 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
       // so their latency overlaps the MFMAs in flight and the softmax
       constexpr int NK = C::KC / 16 * QF;
       s16x8 kf[C::KC / 16][QF];
-#pragma unroll
-      for (int m = 0; m < C::KC / 16; ++m)
-#pragma unroll
-        for (int ks = 0; ks < QF; ++ks) {
-          const int row = 16 * m + p;
-          kf[m][ks] = lds_read_b128(Ks + (row * C::CPR + ((4 * ks + g) ^ swz(row, C::CPR))) * 16);
-        }
+      const unsigned ksu = (unsigned)(uintptr_t)Ks;
+      static_for<NK>([&](auto F) {
+        constexpr int m = decltype(F)::value / QF, ks = decltype(F)::value % QF;
+        kf[m][ks] = lds_read_b128_at<(ks / 4) * 256 + m * 256 * C::CPR>(ksu + kbl[ks % 4]);
+      });
 #pragma unroll
       for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll

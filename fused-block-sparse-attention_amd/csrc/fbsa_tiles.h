@@ -41,23 +41,41 @@ template <typename T, int D> struct RowFrag {
 template <typename T, int D, int NM, int W = 0>
 __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
-  if constexpr (sizeof(T) == 2 && W > 0) {
-    constexpr int KS = D / 32, NK = NM * KS;
-    s16x8 x[NK];
-    auto rd = [&](int k) {
-      const int row = 16 * (k / KS) + p;
-      x[k] = lds_read_b128(tile + (row * CPR + ((4 * (k % KS) + g) ^ swz(row, CPR))) * 16);
-    };
+  if constexpr (sizeof(T) == 2) {
+    // read (m, ks) at lane base kb[ks % 4] + (ks / 4) * 256 + m * 256 * CPR
+    constexpr int KS = D / 32, NK = NM * KS, KL = KS < 4 ? KS : 4;
+    if constexpr (W > 0) {
+      unsigned kb[KL];
 #pragma unroll
-    for (int k = 0; k < (W < NK ? W : NK); ++k) rd(k);
+      for (int l = 0; l < KL; ++l) kb[l] = (unsigned)(uintptr_t)tile + tile_kbase(l, g, p, CPR);
+      s16x8 x[NK];
+      auto rd = [&](auto K) {
+        constexpr int k = decltype(K)::value, m = k / KS, ks = k % KS;
+        x[k] = lds_read_b128_at<(ks / 4) * 256 + m * 256 * CPR>(kb[ks % 4]);
+      };
+      static_for<(W < NK ? W : NK)>(rd);
+      static_for<NK>([&](auto K) {
+        constexpr int k = decltype(K)::value;
+        constexpr int last = k + W - 1 < NK - 1 ? k + W - 1 : NK - 1;  // last read issued so far
+        lds_wait_le<(last - k < 15 ? last - k : 15)>();
+        lds_ready(x[k]);
+        if constexpr (k % KS == 0) acc[k / KS] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[k / KS] = Mfma16<T>::run(x[k], fr.h[k % KS], acc[k / KS]);
+        if constexpr (k + W < NK) rd(std::integral_constant<int, k + W>{});
+      });
+    } else {
+      const char *kb[KL];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int last = k + W - 1 < NK - 1 ? k + W - 1 : NK - 1;  // last read issued so far
-      lds_wait_upto(last - k);
-      lds_ready(x[k]);
-      if (k % KS == 0) acc[k / KS] = f32x4{0.f, 0.f, 0.f, 0.f};
-      acc[k / KS] = Mfma16<T>::run(x[k], fr.h[k % KS], acc[k / KS]);
-      if (k + W < NK) rd(k + W);
+      for (int l = 0; l < KL; ++l) kb[l] = tile + tile_kbase(l, g, p, CPR);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const s16x8 x = *(const s16x8 *)(kb[ks % 4] + (ks / 4) * 256 + m * 256 * CPR);
+          acc[m] = Mfma16<T>::run(x, fr.h[ks], acc[m]);
+        }
+      }
     }
     return;
   }
@@ -65,23 +83,15 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
   for (int m = 0; m < NM; ++m) {
     acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int row = 16 * m + p;
-    if constexpr (sizeof(T) == 4) {
 #pragma unroll
-      for (int ks = 0; ks < D / 4; ++ks) {
-        const float x = *(const float *)(tile + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
-        acc[m] = mfma_f32_16x16x4(x, fr.f[ks], acc[m]);
-        if constexpr (D >= 256) if (ks % 16 == 15) asm volatile("" ::: "memory");  // at most 16 loads ahead
-      }
-      // keeps the next row tile's loads from being hoisted above these MFMAs
-      // (at d >= 128 the hoisted loads of every tile exhaust the registers)
-      if constexpr (D >= 128) asm volatile("" ::: "memory");
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < D / 32; ++ks) {
-        const s16x8 x = *(const s16x8 *)(tile + (row * CPR + ((4 * ks + g) ^ swz(row, CPR))) * 16);
-        acc[m] = Mfma16<T>::run(x, fr.h[ks], acc[m]);
-      }
+    for (int ks = 0; ks < D / 4; ++ks) {
+      const float x = *(const float *)(tile + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
+      acc[m] = mfma_f32_16x16x4(x, fr.f[ks], acc[m]);
+      if constexpr (D >= 256) if (ks % 16 == 15) asm volatile("" ::: "memory");  // at most 16 loads ahead
     }
+    // keeps the next row tile's loads from being hoisted above these MFMAs
+    // (at d >= 128 the hoisted loads of every tile exhaust the registers)
+    if constexpr (D >= 128) asm volatile("" ::: "memory");
   }
 }
 
@@ -100,23 +110,26 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
       pk[k2] = pack8<T>(y);
     }
     constexpr int NTL = D / 16, RPT = 2 * (KC / 32);  // output tiles, reads per tile
-    constexpr int W = TW < NTL ? TW : NTL;
+    constexpr int W = TW < NTL ? TW : NTL, VL = NTL < 8 ? NTL : 8;
     s16x4 lo[NTL][KC / 32], hi[NTL][KC / 32];
-    auto rd = [&](int t) {
-      const int cb = 2 * t + ((p & 3) >> 1);
+    // tile t, rows 32 k2 + 4g + p/4 (+16): lane base vb[t % 8] plus a constant
+    unsigned vb[VL];
 #pragma unroll
-      for (int k2 = 0; k2 < KC / 32; ++k2) {
-        const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
-        lo[t][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
-        hi[t][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
-      }
+    for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
+    auto rd = [&](auto TT) {
+      constexpr int t = decltype(TT)::value;
+      static_for<KC / 32>([&](auto K2) {
+        constexpr int k2 = decltype(K2)::value, off = (t / 8) * 256 + k2 * 512 * CPR;
+        lo[t][k2] = lds_read_tr16_at<off>(vb[t % 8]);
+        hi[t][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[t % 8]);
+      });
     };
-#pragma unroll
-    for (int t = 0; t < W; ++t) rd(t);
-#pragma unroll
-    for (int t = 0; t < NTL; ++t) {
-      const int last = t + W - 1 < NTL - 1 ? t + W - 1 : NTL - 1;  // last tile requested so far
-      lds_wait_upto((last - t) * RPT);
+    static_for<W>(rd);
+    static_for<NTL>([&](auto TT) {
+      constexpr int t = decltype(TT)::value;
+      constexpr int last = t + W - 1 < NTL - 1 ? t + W - 1 : NTL - 1;  // last tile requested so far
+      constexpr int n = (last - t) * RPT;
+      lds_wait_le<(n < 15 ? n : 15)>();
 #pragma unroll
       for (int k2 = 0; k2 < KC / 32; ++k2) {
         lds_ready(lo[t][k2]);
@@ -125,8 +138,8 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
         const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         acc[t] = Mfma16<T>::run(av, pk[k2], acc[t]);
       }
-      if (t + W < NTL) rd(t + W);
-    }
+      if constexpr (t + W < NTL) rd(std::integral_constant<int, t + W>{});
+    });
     return;
   }
   if constexpr (sizeof(T) == 4) {
@@ -156,20 +169,22 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
     // the transposed reads go out in batches of up to 8 output tiles (all of
     // them for d <= 128), each batch waited for once, so d = 256 does not hold
     // every tile's operands in registers at the same time
-    constexpr int TB = D / 16 < 8 ? D / 16 : 8;
+    constexpr int TB = D / 16 < 8 ? D / 16 : 8, VL = TB;
+    unsigned vb[VL];
+#pragma unroll
+    for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
 #pragma unroll
     for (int t0 = 0; t0 < D / 16; t0 += TB) {
       s16x4 lo[TB][KC / 32], hi[TB][KC / 32];
-#pragma unroll
-      for (int tt = 0; tt < TB; ++tt) {
-        const int cb = 2 * (t0 + tt) + ((p & 3) >> 1);
-#pragma unroll
-        for (int k2 = 0; k2 < KC / 32; ++k2) {
-          const int ra = 32 * k2 + 4 * g + (p >> 2), rb = ra + 16;
-          lo[tt][k2] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
-          hi[tt][k2] = lds_read_tr16(tile + (rb * CPR + (cb ^ swz(rb, CPR))) * 16 + (p & 1) * 8);
-        }
-      }
+      static_for<TB>([&](auto TT) {
+        constexpr int tt = decltype(TT)::value;
+        static_for<KC / 32>([&](auto K2) {
+          constexpr int k2 = decltype(K2)::value, off = k2 * 512 * CPR;
+          // tile t0 + tt: lane base vb[tt] (t0 is a multiple of 8) plus (t0 / 8) * 256
+          lo[tt][k2] = lds_read_tr16_at<off>(vb[tt] + (t0 / 8) * 256);
+          hi[tt][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[tt] + (t0 / 8) * 256);
+        });
+      });
       lds_wait_all();
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt)
