@@ -512,11 +512,22 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 
   const T *kbase = (const T *)a.k + b * a.sk[0] + hk * a.sk[1];
   const T *vbase = (const T *)a.v + b * a.sv[0] + hk * a.sv[1];
+  // d > 64: a per-thread copy plan (offsets computed once, uniform row-0
+  // bases per chunk); d <= 64 keeps the per-issue addressing (fewer registers,
+  // four workgroups per CU)
+  TilePairPlan<T, C::KC, D, C::NW, C::LPT> plan;
+  if constexpr (D > 64) plan.init(a.sk[2], a.sv[2], w, lane);
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
-    const int64_t row0 = (int64_t)blk_of(slot) * BS + ch * C::KC;
-    issue_tile_pair<T, C::KC, D, C::NW, C::LPT, (D <= 64)>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2], vbase,
-                                                a.sv[2], row0, w, lane);
+    if constexpr (D > 64) {
+      const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(blk_of(slot) * BS + ch * C::KC);
+      plan.template issue<false>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, (const char *)(kbase + row0 * a.sk[2]),
+                                 (const char *)(vbase + row0 * a.sv[2]), w);
+    } else {
+      const int64_t row0 = (int64_t)blk_of(slot) * BS + ch * C::KC;
+      issue_tile_pair<T, C::KC, D, C::NW, C::LPT, true>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2],
+                                                        vbase, a.sv[2], row0, w, lane);
+    }
   };
 
   f32x4 dqacc[D / 16];
@@ -553,24 +564,54 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
     mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Vs, df, dpacc, g, p);  // dP^T
 
-    int lim = 1 << 30;
+    const float off = gt - lse2;
+    float ds[C::KC / 16][4];
+    if constexpr (D <= 64) {
+      // (the select form keeps fewer registers live: four workgroups per CU)
+      int lim = 1 << 30;
+      if (kind != KIND_FULL) {
+        const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
+                              : kind == KIND_PAD  ? a.l_valid - j * BS - 1
+                                                  : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
+                                                                                                : a.l_valid - j * BS - 1);
+        lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
+      }
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = (16 * m + r <= lim) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off)) : 0.f;
+          ds[m][r] = pv * (dpacc[m][r] - delta);
+        }
+    } else {
+#pragma unroll
+    for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off));
+        ds[m][r] = pv * (dpacc[m][r] - delta);
+      }
+    // masked keys (key row 16m + r of the chunk valid iff <= lim): a uniform
+    // branch, so unmasked chunks (the common case) skip the compares
     if (kind != KIND_FULL) {
       const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
                             : kind == KIND_PAD  ? a.l_valid - j * BS - 1
                                                 : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
                                                                                               : a.l_valid - j * BS - 1);
-      lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
+      const int lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * m + r > lim) ds[m][r] = 0.f;
     }
-    const float off = gt - lse2;
-    float ds[C::KC / 16][4];
+    }
+    if (want_dg) {
 #pragma unroll
-    for (int m = 0; m < C::KC / 16; ++m)
+      for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv = (16 * m + r <= lim) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off)) : 0.f;
-        ds[m][r] = pv * (dpacc[m][r] - delta);
-        dgl += ds[m][r];
-      }
+        for (int r = 0; r < 4; ++r) dgl += ds[m][r];
+    }
     if (want_dg && ch == C::NCH - 1) {
 #pragma unroll
       for (int x = 1; x < 64; x <<= 1) dgl += shfl_xor_f(dgl, x);
@@ -790,7 +831,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
       const char *db = (const char *)a.dout + (b * a.sdo[0] + hq * a.sdo[1] + row0 * a.sdo[2]) * C::ES;
       char *st = stages + istg * C::STAGE_BYTES;
 #pragma unroll
-      for (int n = 0; n < C::LPT; ++n) g2lds16((tdo[n] ? db : qb) + toff[n], st + (n * C::NW + w) * 1024);
+      for (int n = 0; n < C::LPT; ++n) g2lds16_s(tdo[n] ? db : qb, (unsigned)toff[n], st + (n * C::NW + w) * 1024);
       // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
       if (lane < C::KC / (2 * C::NW))
         g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + w * (C::KC / C::NW) + 2 * lane,

@@ -69,6 +69,21 @@ __device__ __forceinline__ void g2lds16(const void *gsrc, void *lds_wave_base) {
   const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(m) : "memory", "m0");
 }
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (the instruction's saddr form): no 64-bit address VALU op per load.
+__device__ __forceinline__ void g2lds16_s(const void *sbase, unsigned voff, void *lds_wave_base) {
+  const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
+  // the base is uniform by contract; readfirstlane puts it in SGPRs (folded away
+  // when the compiler already holds it there)
+  // (readfirstlane returns int: each half goes through uint32_t so that the
+  // low word is zero-extended, never sign-extended, into the 64-bit base)
+  const uint64_t bp = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((unsigned)(bp >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((unsigned)bp);
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sb), "s"(m)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void g2lds4(const void *gsrc, void *lds_wave_base) {
   const unsigned m = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gsrc), "s"(m) : "memory", "m0");

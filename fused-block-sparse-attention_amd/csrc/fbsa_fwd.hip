@@ -189,7 +189,7 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int n = 0; n < C::LPT; ++n) {
       const bool part = (n * C::NW + w) * 64 >= C::KC * C::CPR;  // wave-uniform
-      g2lds16((part ? vb : kb) + doff[n], st + (n * C::NW + w) * 1024);
+      g2lds16_s(part ? vb : kb, (unsigned)doff[n], st + (n * C::NW + w) * 1024);
     }
   };
 

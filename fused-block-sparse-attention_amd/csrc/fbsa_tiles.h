@@ -217,6 +217,38 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
   }
 }
 
+// Per-thread plan of the direct-to-LDS copy of a KC-row tile pair (the loads
+// of issue_tile_pair): load n reads byte off[n] of source part[n]'s first row
+// (part[n] is uniform across a wave). Computed once; each issue then needs only
+// the two sources' row-0 addresses.
+template <typename T, int KC, int D, int NW, int LPT> struct TilePairPlan {
+  uint32_t off[LPT];
+  bool part[LPT];
+  __device__ __forceinline__ void init(int64_t stride0, int64_t stride1, int w, int lane) {
+    constexpr int CPR = D * (int)sizeof(T) / 16;
+#pragma unroll
+    for (int n = 0; n < LPT; ++n) {
+      const int u = (n * NW + w) * 64 + lane;
+      const int pt = u / (KC * CPR);
+      const int rem = u - pt * (KC * CPR);
+      const int row = rem / CPR, pos = rem % CPR;
+      part[n] = pt != 0;
+      off[n] = (uint32_t)(((int64_t)row * (pt ? stride1 : stride0) + (pos ^ swz(row, CPR)) * (16 / (int)sizeof(T))) *
+                          (int64_t)sizeof(T));
+    }
+  }
+  // src0 / src1: the first rows of the chunk (wave-uniform)
+  template <bool TRACKED>
+  __device__ __forceinline__ void issue(char *st, const char *src0, const char *src1, int w) const {
+#pragma unroll
+    for (int n = 0; n < LPT; ++n) {
+      const char *base = part[n] ? src1 : src0;
+      if constexpr (TRACKED) g2lds16_tracked(base + off[n], st + (n * NW + w) * 1024);
+      else g2lds16_s(base, off[n], st + (n * NW + w) * 1024);
+    }
+  }
+};
+
 // Copy KC rows from each of two row-major sources into one LDS stage (two
 // swizzled tiles back to back) with direct-to-LDS 16-byte loads; every thread
 // issues LPT loads. Rows are src + (row0 + r) * stride. TRACKED: through the
