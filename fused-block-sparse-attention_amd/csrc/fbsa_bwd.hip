@@ -49,6 +49,11 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_DQ_WIN
 #define FBSA_DQ_WIN 8
 #endif
+// dQ walks a row's key blocks in ascending block index (lists of up to 64
+// valid slots; more L2 hits on the gathered K/V tiles)
+#ifndef FBSA_DQ_SORT
+#define FBSA_DQ_SORT 1
+#endif
 #ifndef FBSA_DKDV_WIN
 #define FBSA_DKDV_WIN 8
 #endif
@@ -489,6 +494,26 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
       nout += __popcll(m);
     }
     if (lane == 0) s_nvalid = nout;
+    if (FBSA_DQ_SORT && nout > 1 && nout <= 64) {
+      // ascending key blocks, as the forward walks them; equal blocks keep their
+      // slot order, and the slot -> entry map follows the permutation
+      int j = 0x7fffffff, kind = 0;
+      float gt = 0.f;
+      if (lane < nout) { j = s_blk[lane]; kind = s_kind[lane]; gt = s_gate[lane]; }
+      int rank = 0;
+      for (int m = 0; m < nout; ++m) {
+        const int jm = s_blk[m];
+        rank += jm < j || (jm == j && m < lane);
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (lane < nout) { s_blk[rank] = j; s_kind[rank] = kind; s_gate[rank] = gt; }
+      for (int s0 = 0; s0 < a.kk; s0 += 64) {
+        const int s = s0 + lane;
+        const int c = s < a.kk ? s_cidx[s] : -1;
+        const int rc = __shfl(rank, c < 0 ? 0 : c);
+        if (c >= 0) s_cidx[s] = rc;
+      }
+    }
   }
 
   const int tq = w * 16 + p;

@@ -57,6 +57,14 @@ template <typename T, int BS, int D, int QT = 1, int KCO = 0, int NSO = 0> struc
 #define FBSA_FWD_KFIRST 1
 #endif
 
+// Walk a row's selected key blocks in ascending block index (lists of up to 64
+// valid slots). The softmax does not depend on the order; the workgroups that
+// run together on an XCD then read nearby key blocks at about the same time,
+// so more of the gathered K/V tiles are L2 hits.
+#ifndef FBSA_FWD_SORT
+#define FBSA_FWD_SORT 1
+#endif
+
 template <int N> __device__ __forceinline__ void wait_pending(int pending_chunks) {
   // wait until at most pending_chunks * LPT DMA loads are outstanding (N = LPT)
   switch (pending_chunks) {
@@ -130,6 +138,19 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
       nout += __popcll(m);
     }
     if (lane == 0) s_nvalid = nout;
+    if (FBSA_FWD_SORT && nout > 1 && nout <= 64) {
+      // rank of each entry by (block, slot); equal blocks keep their slot order
+      int j = 0x7fffffff, kind = 0;
+      float gt = 0.f;
+      if (lane < nout) { j = s_blk[lane]; kind = s_kind[lane]; gt = s_gate[lane]; }
+      int rank = 0;
+      for (int m = 0; m < nout; ++m) {
+        const int jm = s_blk[m];
+        rank += jm < j || (jm == j && m < lane);
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (lane < nout) { s_blk[rank] = j; s_kind[rank] = kind; s_gate[rank] = gt; }
+    }
   }
 
   // ---- 2. Q fragments (B operands of S^T = K Q^T), one per query tile ----
