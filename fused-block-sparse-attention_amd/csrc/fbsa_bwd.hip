@@ -537,22 +537,16 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 
   const T *kbase = (const T *)a.k + b * a.sk[0] + hk * a.sk[1];
   const T *vbase = (const T *)a.v + b * a.sv[0] + hk * a.sv[1];
-  // d > 64: a per-thread copy plan (offsets computed once, uniform row-0
-  // bases per chunk); d <= 64 keeps the per-issue addressing (fewer registers,
-  // four workgroups per CU)
+  // a per-thread copy plan (offsets computed once, uniform row-0 bases per
+  // chunk); d <= 64 issues through the compiler builtin (four workgroups per
+  // CU, measured faster there than the asm form), d > 64 through the asm form
   TilePairPlan<T, C::KC, D, C::NW, C::LPT> plan;
-  if constexpr (D > 64) plan.init(a.sk[2], a.sv[2], w, lane);
+  plan.init(a.sk[2], a.sv[2], w, lane);
   auto issue = [&](int c) {
     const int slot = c / C::NCH, ch = c % C::NCH;
-    if constexpr (D > 64) {
-      const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(blk_of(slot) * BS + ch * C::KC);
-      plan.template issue<false>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, (const char *)(kbase + row0 * a.sk[2]),
-                                 (const char *)(vbase + row0 * a.sv[2]), w);
-    } else {
-      const int64_t row0 = (int64_t)blk_of(slot) * BS + ch * C::KC;
-      issue_tile_pair<T, C::KC, D, C::NW, C::LPT, true>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, kbase, a.sk[2],
-                                                        vbase, a.sv[2], row0, w, lane);
-    }
+    const int64_t row0 = (int64_t)__builtin_amdgcn_readfirstlane(blk_of(slot) * BS + ch * C::KC);
+    plan.template issue<(D <= 64)>(stages + (c % C::NSTAGE) * C::STAGE_BYTES, (const char *)(kbase + row0 * a.sk[2]),
+                                   (const char *)(vbase + row0 * a.sv[2]), w);
   };
 
   f32x4 dqacc[D / 16];
@@ -591,24 +585,6 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 
     const float off = gt - lse2;
     float ds[C::KC / 16][4];
-    if constexpr (D <= 64) {
-      // (the select form keeps fewer registers live: four workgroups per CU)
-      int lim = 1 << 30;
-      if (kind != KIND_FULL) {
-        const int64_t lim64 = kind == KIND_DIAG ? (int64_t)tq
-                              : kind == KIND_PAD  ? a.l_valid - j * BS - 1
-                                                  : ((i - j) * BS + tq < a.l_valid - j * BS - 1 ? (i - j) * BS + tq
-                                                                                                : a.l_valid - j * BS - 1);
-        lim = (int)(lim64 < -1 ? -1 : lim64) - ch * C::KC - 4 * g;
-      }
-#pragma unroll
-      for (int m = 0; m < C::KC / 16; ++m)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pv = (16 * m + r <= lim) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off)) : 0.f;
-          ds[m][r] = pv * (dpacc[m][r] - delta);
-        }
-    } else {
 #pragma unroll
     for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
@@ -629,7 +605,6 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (16 * m + r > lim) ds[m][r] = 0.f;
-    }
     }
     if (want_dg) {
 #pragma unroll
@@ -1053,21 +1028,25 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
         mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p);  // dP
         float pp[HR / 16][4], ds[HR / 16][4];
-        // every exponential is computed and masked by a select: a conditional
-        // exponential becomes a branch per element, each waiting for its own
-        // row-statistics read
+        // every exponential is computed unconditionally; masked elements of
+        // a masked chunk kind are then replaced by zeros in one uniform branch
+        // (unmasked chunks, the common case, skip the compares)
 #pragma unroll
         for (int m = 0; m < HR / 16; ++m)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float2 ms = Mh[16 * m + 4 * g + r];
-            const bool ok = kok && (16 * m + r >= th);
-            float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x));
-            asm volatile("" : "+v"(ev));
-            const float pv = ok ? ev : 0.f;
-            pp[m][r] = pv;
-            ds[m][r] = pv * (dpacc[m][r] - ms.y);
+            const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x));
+            pp[m][r] = ev;
+            ds[m][r] = ev * (dpacc[m][r] - ms.y);
           }
+        if (kind != KIND_FULL) {
+#pragma unroll
+          for (int m = 0; m < HR / 16; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (!(kok && (16 * m + r >= th))) { pp[m][r] = 0.f; ds[m][r] = 0.f; }
+        }
         mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Dh, pp, dvacc, g, p);  // dV^T += dO^T P
         mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Qh, ds, dkacc, g, p);  // dK^T += Q^T dS
       }

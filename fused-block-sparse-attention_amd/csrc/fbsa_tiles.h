@@ -217,10 +217,11 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
   }
 }
 
-// Per-thread plan of the direct-to-LDS copy of a KC-row tile pair (the loads
-// of issue_tile_pair): load n reads byte off[n] of source part[n]'s first row
-// (part[n] is uniform across a wave). Computed once; each issue then needs only
-// the two sources' row-0 addresses.
+// Per-thread plan of the direct-to-LDS copy of a KC-row tile pair (two
+// swizzled tiles back to back in one LDS stage, 16-byte loads, LPT per
+// thread): load n reads byte off[n] of source part[n]'s first row (part[n] is
+// uniform across a wave). Computed once; each issue then needs only the two
+// sources' row-0 addresses.
 template <typename T, int KC, int D, int NW, int LPT> struct TilePairPlan {
   uint32_t off[LPT];
   bool part[LPT];
@@ -248,28 +249,5 @@ template <typename T, int KC, int D, int NW, int LPT> struct TilePairPlan {
     }
   }
 };
-
-// Copy KC rows from each of two row-major sources into one LDS stage (two
-// swizzled tiles back to back) with direct-to-LDS 16-byte loads; every thread
-// issues LPT loads. Rows are src + (row0 + r) * stride. TRACKED: through the
-// compiler builtin (g2lds16_tracked) instead of the asm form.
-template <typename T, int KC, int D, int NW, int LPT, bool TRACKED = false>
-__device__ __forceinline__ void issue_tile_pair(char *st, const T *src0, int64_t stride0, const T *src1,
-                                                int64_t stride1, int64_t row0, int w, int lane) {
-  constexpr int CPR = D * (int)sizeof(T) / 16;
-  constexpr int ES = (int)sizeof(T);
-#pragma unroll
-  for (int n = 0; n < LPT; ++n) {
-    const int wl = n * NW + w;
-    const int u = wl * 64 + lane;
-    const int part = u / (KC * CPR);
-    const int rem = u - part * (KC * CPR);
-    const int row = rem / CPR, pos = rem % CPR;
-    const int chunk = pos ^ swz(row, CPR);
-    const T *src = part ? src1 + (row0 + row) * stride1 : src0 + (row0 + row) * stride0;
-    if constexpr (TRACKED) g2lds16_tracked(src + chunk * (16 / ES), st + wl * 1024);
-    else g2lds16(src + chunk * (16 / ES), st + wl * 1024);
-  }
-}
 
 }  // namespace fbsa
