@@ -715,7 +715,11 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   int4 *s_meta = (int4 *)(smem + C::NSTAGE * C::STAGE_BYTES);  // per entry: query block, mask kind, gate bits
   float4 *s_xch = (float4 *)(s_meta + MAXE);  // two roles: P of each key group's part, [HR/16][KEYS/16][64 lanes]
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
+  // one role per wave: the wave index as a scalar (its tile-part selects and
+  // copy bases then stay on the scalar unit; measured 3% faster at d 64, slower
+  // for the two-role kernels)
+  const int tid = threadIdx.x, w = ROLES == 1 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6, lane = tid & 63,
+            g = lane >> 4, p = lane & 15;
   // Launch order. Causal selection gives low key blocks far longer transposed
   // lists than high ones. When every XCD's contiguous share of the (b, KV head,
   // block) units is whole rows of key blocks, the shares carry equal work and
@@ -792,7 +796,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
     const int rem = u - part * (C::KC * C::CPR);
     const int row = rem / C::CPR, pos = rem % C::CPR;
     toff[n] = (int32_t)(((int64_t)row * (part ? a.sdo[2] : a.sq[2]) + (pos ^ swz(row, C::CPR)) * (16 / C::ES)) * C::ES);
-    tdo[n] = part != 0;
+    tdo[n] = (n * C::NW + w) * 64 >= C::KC * C::CPR;  // == (part != 0), uniform across the wave
   }
 
   // dense lists: entry at position e of block j's list is query block dense_i0 + e
@@ -982,7 +986,8 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 
       // the chunk's query rows in parts of HR (32) rows, one after the other:
       // the per-part S, dP, P, dS and row statistics stay in few registers
-#pragma unroll 1
+      // (unrolled at d <= 64: the parts' LDS addresses become instruction offsets)
+#pragma unroll(D <= 64 ? 2 : 1)
       for (int h = 0; h < C::KC / HR; ++h) {
         const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
         const float2 *Mh = Ms + h * HR;

@@ -233,7 +233,7 @@ template <typename T, int KC, int D, int NW, int LPT> struct TilePairPlan {
       const int pt = u / (KC * CPR);
       const int rem = u - pt * (KC * CPR);
       const int row = rem / CPR, pos = rem % CPR;
-      part[n] = pt != 0;
+      part[n] = (n * NW + w) * 64 >= KC * CPR;  // == (pt != 0), uniform across the wave
       off[n] = (uint32_t)(((int64_t)row * (pt ? stride1 : stride0) + (pos ^ swz(row, CPR)) * (16 / (int)sizeof(T))) *
                           (int64_t)sizeof(T));
     }
