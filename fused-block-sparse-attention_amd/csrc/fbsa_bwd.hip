@@ -987,7 +987,8 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
       // the chunk's query rows in parts of HR (32) rows, one after the other:
       // the per-part S, dP, P, dS and row statistics stay in few registers
       // (unrolled at d <= 64: the parts' LDS addresses become instruction offsets)
-#pragma unroll(D <= 64 ? 2 : 1)
+      constexpr int HUNROLL = D <= 64 ? 2 : 1;
+#pragma unroll HUNROLL
       for (int h = 0; h < C::KC / HR; ++h) {
         const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
         const float2 *Mh = Ms + h * HR;
