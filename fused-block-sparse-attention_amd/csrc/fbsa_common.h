@@ -284,17 +284,20 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
 // them. Returns the unit of launch order bid and sets the head within the
 // group; with grp == 1 it is the identity. Units past the last full round of 8
 // map in launch order.
+// (launch indices and unit counts are below 2^31, a grid's x limit: 32-bit
+// division, a short sequence, instead of the long 64-bit expansion)
 __device__ __forceinline__ int64_t gqa_unit(int64_t bid, int64_t nunits, int grp, int *hin) {
-  const int64_t full = nunits / 8 * 8;
-  const int64_t base = full * grp;
-  if (bid >= base) {
-    const int64_t r = bid - base;
-    *hin = (int)(r % grp);
-    return full + r / grp;
+  const uint32_t b32 = (uint32_t)bid, g = (uint32_t)grp;
+  const uint32_t full = (uint32_t)nunits / 8u * 8u;
+  const uint32_t base = full * g;
+  if (b32 >= base) {
+    const uint32_t r = b32 - base;
+    *hin = (int)(r % g);
+    return (int64_t)(full + r / g);
   }
-  const int64_t s = bid / 8;
-  *hin = (int)(s % grp);
-  return (s / grp) * 8 + bid % 8;
+  const uint32_t s = b32 / 8u;
+  *hin = (int)(s % g);
+  return (int64_t)((s / g) * 8u + b32 % 8u);
 }
 
 }  // namespace fbsa

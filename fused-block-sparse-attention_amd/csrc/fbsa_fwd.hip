@@ -95,9 +95,11 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   // tiles)
   int hin;
   int64_t t = gqa_unit(blockIdx.x, (int64_t)gridDim.x / a.grp, a.grp, &hin);
-  const int64_t i = a.i0 + t % a.ni; t /= a.ni;
-  const int hk = (int)(t % a.Hkv);
-  const int64_t b = t / a.Hkv;
+  // (32-bit division: launch indices are below 2^31)
+  const uint32_t t32 = (uint32_t)t;
+  const int64_t i = a.i0 + t32 % (uint32_t)a.ni;
+  const int hk = (int)(t32 / (uint32_t)a.ni % (uint32_t)a.Hkv);
+  const int64_t b = t32 / (uint32_t)a.ni / (uint32_t)a.Hkv;
   const int hq = hk * a.grp + hin;
   const int hs = a.hsel == 1 ? 0 : hk;
 
