@@ -75,18 +75,6 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_DKDV_LDS_BUDGET
 #define FBSA_DKDV_LDS_BUDGET 40960
 #endif
-// dQ at 16-bit d 64: 32-key chunks through a two-stage ring of 16 KB, so that
-// the kernel fits 77 VGPRs and LDS for five or more workgroups per CU (measured
-// 9% faster at configuration 3 than 64-key chunks at four workgroups per CU)
-#ifndef FBSA_DQ_KC64
-#define FBSA_DQ_KC64 32
-#endif
-#ifndef FBSA_DQ_LDS_BUDGET64
-#define FBSA_DQ_LDS_BUDGET64 16384
-#endif
-#ifndef FBSA_DQ_MINWG64
-#define FBSA_DQ_MINWG64 5
-#endif
 
 static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -434,7 +422,7 @@ template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct
   static constexpr int NW = ROWS / 16;
   static constexpr int NT = NW * 64;
   // key / query rows per chunk: 64, 32 at d 256 (16-bit), 16 for fp32 at d >= 128 (registers)
-  static constexpr int KCW = ES == 4 && D >= 128 ? 16 : (D >= 256 ? 32 : (D == 64 && !META && ES == 2 ? FBSA_DQ_KC64 : 64));
+  static constexpr int KCW = ES == 4 && D >= 128 ? 16 : (D >= 256 ? 32 : 64);
   static constexpr int KC = BS < KCW ? BS : KCW;
   static constexpr int NCH = BS / KC;
   static constexpr int CPR = D * ES / 16;
@@ -448,13 +436,9 @@ template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
 };
 
-template <typename T, int D> constexpr int dq_lds_budget() {
-  return D == 64 && sizeof(T) == 2 ? FBSA_DQ_LDS_BUDGET64 : FBSA_DQ_LDS_BUDGET;
-}
-
 template <typename T, int BS, int D, bool DENSE = false>
-__global__ __launch_bounds__(BS * 4, (BS == 64 && D == 64 && sizeof(T) == 2 ? FBSA_DQ_MINWG64 : 1)) void dq_kernel(BwdArgs a) {
-  using C = BwdCfg<T, BS, D, dq_lds_budget<T, D>(), 0>;
+__global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
+  using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
   int *s_blk = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
@@ -1257,7 +1241,7 @@ template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, co
 }
 
 template <typename T, int BS, int D, bool DENSE> static int launch_dq_as(const BwdArgs &a, hipStream_t s) {
-  using C = BwdCfg<T, BS, D, dq_lds_budget<T, D>(), 0>;
+  using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
   static size_t granted = 0;
   int e = set_lds(dq_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dq");
