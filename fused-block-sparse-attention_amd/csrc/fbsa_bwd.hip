@@ -1162,16 +1162,22 @@ template <typename T>
 __global__ __launch_bounds__(256) void dkdv_reduce_kernel(const int32_t *wi_slot, const uint64_t *pos,
                                                           const float *partials, void *dk, void *dv, int64_t nblk,
                                                           int64_t Hkv, int64_t L, int64_t bs, int64_t D, float scale) {
+  // grid: x = work item, y = a slice of 2048 of its 2 bs D elements (one
+  // 8-element group per thread), so that a block split into many segments is
+  // summed by many workgroups, each with several segments' loads in flight
   const int64_t wi = blockIdx.x;
   const int slot0 = wi_slot[wi];
   if (slot0 < 0) return;
+  const int64_t n = bs * D;  // a multiple of 8: an 8-element group lies in dK or in dV
+  const int64_t x = 8 * ((int64_t)blockIdx.y * 256 + threadIdx.x);
+  if (x >= 2 * n) return;
   const int ns = (int)((pos[wi + 1] - pos[wi]) & 0xffffffffu);
   const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
-  const int64_t n = bs * D;  // a multiple of 8: an 8-element group lies in dK or in dV
-  for (int64_t x = 8 * (int64_t)threadIdx.x; x < 2 * n; x += 8 * 256) {
+  {
     const int which = x >= n;  // 0: dK, 1: dV
     const int64_t e = x - which * n;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
     for (int s = 0; s < ns; ++s) {
       const float *src = partials + ((int64_t)(slot0 + s) * 2 + which) * n + e;
       const f32x4 p0 = *(const f32x4 *)src, p1 = *(const f32x4 *)(src + 4);
@@ -1348,7 +1354,7 @@ int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, c
     a.seg_entries_xub = lay.xub;
   }
   if ((e = bwd_dispatch(d, a, false, s)) || !lay.seg_entries) return e;
-  const dim3 g((unsigned)lay.nwi), blk(256);
+  const dim3 g((unsigned)lay.nwi, (unsigned)((2 * d->bs * d->D + 8 * 256 - 1) / (8 * 256))), blk(256);
   const uint64_t *pos = (const uint64_t *)(ws + lay.seg_pos);
   const float *part = (const float *)(ws + lay.partials);
   const int32_t *wsl = (const int32_t *)(ws + lay.wi_slot);
