@@ -229,7 +229,16 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   const int c = tid % TPR;
   float acc = 0.f;
   if (row < a.rows) {
-    const int64_t t = row % a.L, bh = row / a.L, h = bh % a.Hq, b = bh / a.Hq;
+    int64_t t, h, b;
+    if (a.rows < 0x80000000LL) {  // 32-bit division (a short sequence) when the row count allows
+      const uint32_t r32 = (uint32_t)row, bh = r32 / (uint32_t)a.L;
+      t = r32 - bh * (uint32_t)a.L;
+      h = bh % (uint32_t)a.Hq;
+      b = bh / (uint32_t)a.Hq;
+    } else {
+      const int64_t bh = row / a.L;
+      t = row % a.L; h = bh % a.Hq; b = bh / a.Hq;
+    }
     float ov[8], dv[8];
     load8f<T>((const T *)a.o + b * a.so[0] + h * a.so[1] + t * a.so[2] + 8 * c, ov);
     load8f<T>((const T *)a.dout + b * a.sdo[0] + h * a.sdo[1] + t * a.sdo[2] + 8 * c, dv);
