@@ -1171,40 +1171,56 @@ template <typename T>
 __global__ __launch_bounds__(256) void dkdv_reduce_kernel(const int32_t *wi_slot, const uint64_t *pos,
                                                           const float *partials, void *dk, void *dv, int64_t nblk,
                                                           int64_t Hkv, int64_t L, int64_t bs, int64_t D, float scale) {
-  // grid: x = work item, y = a slice of 2048 of its 2 bs D elements (one
-  // 8-element group per thread), so that a block split into many segments is
-  // summed by many workgroups, each with several segments' loads in flight
+  // grid: x = work item, y = a slice of RG * 2048 of its 2 bs D elements (RG
+  // 8-element groups per thread, 256 threads), so that a block split into many
+  // segments is summed by several workgroups with many loads in flight, while an
+  // unsplit item (most of them when lists are short) costs few empty workgroups
+  constexpr int RG = 4;
   const int64_t wi = blockIdx.x;
   const int slot0 = wi_slot[wi];
   if (slot0 < 0) return;
   const int64_t n = bs * D;  // a multiple of 8: an 8-element group lies in dK or in dV
-  const int64_t x = 8 * ((int64_t)blockIdx.y * 256 + threadIdx.x);
-  if (x >= 2 * n) return;
   const int ns = (int)((pos[wi + 1] - pos[wi]) & 0xffffffffu);
   const int64_t j = wi % nblk, hk = (wi / nblk) % Hkv, b = wi / (nblk * Hkv);
-  {
-    const int which = x >= n;  // 0: dK, 1: dV
-    const int64_t e = x - which * n;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int s = 0; s < ns; ++s) {
-      const float *src = partials + ((int64_t)(slot0 + s) * 2 + which) * n + e;
-      const f32x4 p0 = *(const f32x4 *)src, p1 = *(const f32x4 *)(src + 4);
+  int64_t xs[RG];
+  float acc[RG][8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        acc[r] += p0[r];
-        acc[4 + r] += p1[r];
+  for (int gq = 0; gq < RG; ++gq) {
+    xs[gq] = 8 * (((int64_t)blockIdx.y * RG + gq) * 256 + threadIdx.x);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[gq][r] = 0.f;
+  }
+#pragma unroll 2
+  for (int s = 0; s < ns; ++s) {
+    const float *seg = partials + (int64_t)(slot0 + s) * 2 * n;  // dK rows, then dV rows
+#pragma unroll
+    for (int gq = 0; gq < RG; ++gq) {
+      if (xs[gq] < 2 * n) {
+        const f32x4 p0 = *(const f32x4 *)(seg + xs[gq]), p1 = *(const f32x4 *)(seg + xs[gq] + 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[gq][r] += p0[r];
+          acc[gq][4 + r] += p1[r];
+        }
       }
     }
-    const float sc = which ? 1.f : scale;
+  }
 #pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] *= sc;
+  for (int gq = 0; gq < RG; ++gq) {
+    const int64_t x = xs[gq];
+    if (x >= 2 * n) continue;
+    const int which = x >= n;  // 0: dK, 1: dV
+    const int64_t e = x - which * n;
+    const float sc = which ? 1.f : scale;
+    float y[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = acc[gq][r] * sc;
     T *dst = (T *)(which ? dv : dk) + ((b * Hkv + hk) * L + j * bs) * D + e;  // 16-byte aligned
     if constexpr (sizeof(T) == 4) {
-      *(f32x4 *)dst = f32x4{acc[0], acc[1], acc[2], acc[3]};
-      *(f32x4 *)(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+      *(f32x4 *)dst = f32x4{y[0], y[1], y[2], y[3]};
+      *(f32x4 *)(dst + 4) = f32x4{y[4], y[5], y[6], y[7]};
     } else {
-      *(s16x8 *)dst = pack8<T>(acc);
+      *(s16x8 *)dst = pack8<T>(y);
     }
   }
 }
@@ -1363,7 +1379,7 @@ int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, c
     a.seg_entries_xub = lay.xub;
   }
   if ((e = bwd_dispatch(d, a, false, s)) || !lay.seg_entries) return e;
-  const dim3 g((unsigned)lay.nwi, (unsigned)((2 * d->bs * d->D + 8 * 256 - 1) / (8 * 256))), blk(256);
+  const dim3 g((unsigned)lay.nwi, (unsigned)((2 * d->bs * d->D + 4 * 8 * 256 - 1) / (4 * 8 * 256))), blk(256);
   const uint64_t *pos = (const uint64_t *)(ws + lay.seg_pos);
   const float *part = (const float *)(ws + lay.partials);
   const int32_t *wsl = (const int32_t *)(ws + lay.wi_slot);
