@@ -444,6 +444,12 @@ def main():
                             else "pool, select, forward in sequence on one stream")},
         "ms_select": t_sel, "ms_fwd": t_fwd,
         "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,
+        # HBM bytes actually moved per forward launch (rocprofv3 FETCH_SIZE + WRITE_SIZE,
+        # copy-calibrated) over the launch time, against the 8 TB/s peak
+        "fwd_hbm_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
+        "fwd_hbm_frac_of_peak": (traffic_b / (t_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS) if traffic_b else None,
+        # the selection's algorithmic bytes (q and k read once by the pooling) over its time
+        "select_hbm_GBps_algorithmic": (2 * B * H * N * D * 2) / (t_sel * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS,
                      "traffic": traffic_b, "traffic_source": traffic_note,
