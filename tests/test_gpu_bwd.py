@@ -165,6 +165,31 @@ def test_duplicate_heavy_list_segments_half_blocks():
         assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
 
 
+@pytest.mark.parametrize("dtype,D", [("bf16", 64), ("f32", 32)])
+def test_segments_of_small_blocks(dtype, D):
+    # bs 16 with d 64 / 32: a key block's dK and dV hold 2 * 16 * D elements, fewer
+    # than one 8192-element slice of the segment reduction, so most of a reducing
+    # thread's element groups lie past the block. Every content slot of every row
+    # picks block 0 (mask none keeps duplicates): its list has 128 * 8 + 1 = 1025
+    # entries, three segments of at most 512
+    g = torch.Generator().manual_seed(8)
+    B, H, N, bs, kk = 1, 2, 2048, 16, 9
+    nblk = N // bs
+    q, k, v, do = (randn(g, (B, H, N, D), dtype) for _ in range(4))
+    sel = np.zeros((B, 1, nblk, kk), np.int64)
+    sel[..., 0] = np.arange(nblk)
+    got = _gpu_bwd(q, k, v, sel, do, "none")
+    ref = _oracle(q, k, v, sel, do, "none")
+    t = TOL[dtype]
+    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
+        mag = max(1.0, float(np.max(np.abs(rv))))  # block 0 sums 1025 * 16 rows per head
+        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND[dtype] * np.abs(rv)))
+        rl = rel_l2(gv, rv)
+        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
+        bound = t["max_abs"] * (1.0 if dtype == "f32" else mag)
+        assert excess <= bound and rl <= t["rel_l2"], n
+
+
 def test_backward_is_bitwise_repeatable():
     g = torch.Generator().manual_seed(4)
     B, H, N, D, bs, kk = 2, 4, 2048, 64, 64, 9
