@@ -1015,6 +1015,12 @@ __device__ void emit_row(const SelArgs &a, int64_t bh, int64_t i, uint64_t mine,
   }
 }
 
+// ring depth of the tiled selection for 16-bit d <= 64 dot scores: two stages
+// (about 50 KB of LDS, three workgroups per CU) measured faster than four (74 KB,
+// two per CU): 3.01 against 3.92 ms over 65536 blocks, 60 against 61 us over 4096
+#ifndef FBSA_SELT_NST
+#define FBSA_SELT_NST 2
+#endif
 template <typename T, int D, int MODE> struct SelTCfg {
   static constexpr int KS = D / 32;
   static constexpr int NOP = MODE == FBSA_SCORE_DOT ? 1 : 2;
@@ -1024,7 +1030,7 @@ template <typename T, int D, int MODE> struct SelTCfg {
   static constexpr int STB = NOP * OPB + NRMB;   // one ring stage
   static constexpr int LPT = NOP * OPB / (256 * 16);
   static constexpr int CAP = 64;                 // per-row key buffer
-  static constexpr int NST = NOP * OPB <= 8192 ? 4 : 2;  // ring depth: about 74 KB of LDS, 2 workgroups per CU
+  static constexpr int NST = NOP * OPB <= 8192 ? FBSA_SELT_NST : 2;  // ring depth
   static constexpr int OFF_BUF = NST * STB;
   static constexpr int OFF_ROWN = OFF_BUF + 64 * (CAP + 1) * 8;
   static constexpr int OFF_CNT = OFF_ROWN + 2 * 64 * 4;
