@@ -55,12 +55,30 @@ def parse():
                    help="time the two-stream step (selection overlapped with the forward)")
     p.add_argument("--splits", type=int, default=4, help="row ranges of the overlapped step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--min-warmup-s", type=float, default=0.5,
+                   help="continue the untimed warm-up until this much GPU time has run (clock settling)")
     p.add_argument("--cpu-rows", type=int, default=4096, help="query blocks in the CPU sample (4096 = all at config 3)")
     p.add_argument("--qwen", choices=["max", "qmax", "twostage", "lasttok"], default=None,
                    help="time configuration 4 instead (GQA Qwen shape) with this qwen_blocksparse selector")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     return p.parse_args()
+
+
+def warm_up(step, n_min, seconds):
+    """Untimed warm-up: at least n_min steps, continued until `seconds` of GPU
+    work have run (the clock takes some tens of milliseconds of sustained load to
+    settle: the first launches of a cold GPU run up to a third slower). Returns
+    the steps run."""
+    import torch
+    t0, n = time.perf_counter(), 0
+    while n < n_min or time.perf_counter() - t0 < seconds:
+        step()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def calibrate_copy():
@@ -271,9 +289,7 @@ def qwen_main(a):
     def step():
         return qb.blocksparse_forward(q, k, v, selector=S, topk=topk, bs=bs, out_gate=og)
 
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
+    n_warm = warm_up(step, a.warmup, a.min_warmup_s)
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
@@ -297,19 +313,23 @@ def qwen_main(a):
     kk = topk + 2
     flops = 4.0 * B * Hq * nblk * kk * bs * bs * D
     achieved = flops / (t_fwd * 1e-3) / 1e12
+    # HBM counters were taken on the SelectMax indices (other selectors pick other blocks)
+    traffic_b, traffic_note = (traffic_from_profiles("fwd_kernel", f"cfg4_N{N}_Hq{Hq}_Hkv{Hkv}_D{D}_bs{bs}_top{topk}_sink")
+                               if a.qwen == "max" else (None, "measured for SelectMax only"))
     out = {
         "metric": f"select+fwd tokens/s at {N // 1000}k tokens, 1 GPU (bf16, GQA Hq{Hq} Hkv{Hkv} D{D} bs{bs} "
                   f"top-{topk} +own +sink, {type(S).__name__})",
         "value": B * N / (ms_step * 1e-3), "unit": "tokens/s",
-        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": ms_step,
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "warmup_steps_run": n_warm, "ms_per_step": ms_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (q,k,v,g ~ N(0,1), RoPE on q/k dims 0..63, theta 1e7, seed 0, device generator)",
         "config": {"workload": f"BASELINE configs[3]: qwen_blocksparse.{type(S).__name__} + blocksparse_forward "
                                "with the output gate", "B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": D, "block": bs,
                    "nblk": nblk, "topk": topk, "kk": kk},
         "ms_select": t_sel, "ms_fwd": t_fwd,
+        "fwd_hbm_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic_b, "traffic_source": traffic_note,
                      "kernel": "fbsa::fwd_kernel<bf16,128,256>", "flop_per_launch": flops},
         "cpu_baseline": None,
     }
@@ -401,9 +421,7 @@ def main():
             return seq_step(False)
         return pipeline.select_and_attend(q, k, v, bs, topk, need_lse=True, splits=a.splits)
 
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
+    n_warm = warm_up(step, a.warmup, a.min_warmup_s)
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
@@ -432,7 +450,7 @@ def main():
         "metric": (f"select+fwd tokens/s at {N // 1000}k tokens, 1 GPU (bf16, H{H} D{D} bs{bs} top-{topk}, causal)"),
         "value": B * N / (ms_step * 1e-3),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "warmup_steps_run": n_warm,
         "ms_per_step": ms_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (q,k,v ~ N(0,1)/sqrt(D), seed 0, device generator)",
