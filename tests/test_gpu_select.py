@@ -17,13 +17,16 @@ def _say(*a):
     print("[select]", *a, flush=True)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
-def test_pool_mean_tok_then_heads_exact(dtype):
+@pytest.mark.parametrize("dtype,H", [("f32", 4), ("bf16", 4), ("f16", 4),
+                                     ("bf16", 6), ("bf16", 12), ("f16", 13)])
+def test_pool_mean_tok_then_heads_exact(dtype, H):
+    """Mean over tokens, then over H heads. A wave takes heads w, w + 4, ... and
+    loads two of them together: 6, 12 and 13 heads leave waves with an odd count."""
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(0)
-    B, H, N, D, bs = 2, 4, 1000, 64, 64          # N % bs != 0: zero-padded tail block
+    B, N, D, bs = 2, 1000, 64, 64                # N % bs != 0: zero-padded tail block
     x = randn(g, (B, H, N, D), dtype)
-    _say("pool mean_tok_then_grp", dtype)
+    _say("pool mean_tok_then_grp", dtype, H)
     got = np64(selection.pool(x.to(DEV), bs, "mean_tok_then_grp", grp=H))
     ref = osel.pool_mean_tok_then_heads(np64(x), bs, dtype)[:, None]
     assert np.array_equal(got, ref), np.abs(got - ref).max()
