@@ -212,3 +212,20 @@ def test_dense_flag_validation_and_small_backward_workspace():
     assert rows * 8 <= nbytes <= rows * 8 + (16384 + 1) * 4 + 1024
     big.flags = 0   # the same shape as an explicit list would need nblk^2 sort entries: refused
     assert lib.fbsa_bwd_workspace_bytes(big) == 0
+
+
+def test_bench_warm_up_runs_at_least_w_steps_then_until_the_time_floor(monkeypatch):
+    """bench.warm_up: never fewer than W untimed steps; with a time floor it
+    keeps stepping until that much time has passed, and reports the count."""
+    import sys
+    import time
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda: None)
+    calls = []
+    assert bench.warm_up(lambda: calls.append(1), 7, 0.0) == 7 and len(calls) == 7
+    calls.clear()
+    t0 = time.perf_counter()
+    n = bench.warm_up(lambda: (calls.append(1), time.sleep(0.002)), 3, 0.05)
+    assert time.perf_counter() - t0 >= 0.05 and n == len(calls) and n > 3
