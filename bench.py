@@ -81,6 +81,23 @@ def warm_up(step, n_min, seconds):
     return n
 
 
+def roofline_record(flops, alg_bytes, t_ms, kernel, traffic=None, traffic_note=None):
+    """Roofline of one kernel from its algorithmic work: the bound is whichever of
+    the MFMA time (flops / 2.5 PFLOP/s) and the HBM time (compulsory bytes / 8 TB/s)
+    is larger, and `achieved` / `frac` are measured against that bound."""
+    t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12)
+    t_hbm = alg_bytes / (PEAK_HBM_GBS * 1e9)
+    t = t_ms * 1e-3
+    if t_mfma >= t_hbm:
+        rec = {"bound": "mfma", "achieved": flops / t / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        rec = {"bound": "hbm", "achieved": alg_bytes / t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    rec["frac"] = rec["achieved"] / rec["peak"]
+    rec.update({"traffic": traffic, "traffic_source": traffic_note, "kernel": kernel, "flop_per_launch": flops,
+                "algorithmic_bytes_per_launch": alg_bytes, "t_mfma_us": t_mfma * 1e6, "t_hbm_us": t_hbm * 1e6})
+    return rec
+
+
 def calibrate_copy():
     """A plain copy of known size: 1 GiB read + 1 GiB written per launch. Its
     FETCH_SIZE / WRITE_SIZE readings give the counter-to-byte factor."""
@@ -312,7 +329,6 @@ def qwen_main(a):
     t_fwd = sum(x.elapsed_time(y) for x, y in fwd_ev) / a.steps
     kk = topk + 2
     flops = 4.0 * B * Hq * nblk * kk * bs * bs * D
-    achieved = flops / (t_fwd * 1e-3) / 1e12
     # HBM counters were taken on the SelectMax indices (other selectors pick other blocks)
     traffic_b, traffic_note = (traffic_from_profiles("fwd_kernel", f"cfg4_N{N}_Hq{Hq}_Hkv{Hkv}_D{D}_bs{bs}_top{topk}_sink")
                                if a.qwen == "max" else (None, "measured for SelectMax only"))
@@ -327,10 +343,11 @@ def qwen_main(a):
                                "with the output gate", "B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": D, "block": bs,
                    "nblk": nblk, "topk": topk, "kk": kk},
         "ms_select": t_sel, "ms_fwd": t_fwd,
-        "fwd_hbm_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic_b, "traffic_source": traffic_note,
-                     "kernel": "fbsa::fwd_kernel<bf16,128,256>", "flop_per_launch": flops},
+        # L2-miss bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated) per launch over its time:
+        # they count every request the L2s send out, Infinity Cache hits included
+        "fwd_l2miss_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
+        "roofline": roofline_record(flops, 2 * B * Hq * N * D * 2 + 2 * B * Hkv * N * D * 2 + B * Hq * N * D * 2,
+                                    t_fwd, "fbsa::fwd_kernel<bf16,128,256>", traffic_b, traffic_note),
         "cpu_baseline": None,
     }
     if a.bwd:
@@ -438,7 +455,6 @@ def main():
     t_fwd = sum(x.elapsed_time(y) for x, y in fwd_ms) / a.steps
 
     flops = 4.0 * B * H * nblk * kk * bs * bs * D
-    achieved = flops / (t_fwd * 1e-3) / 1e12
     wl = f"cfg3_N{N}_H{H}_D{D}_bs{bs}_top{topk}"
     gathered = B * H * nblk * kk * 2 * bs * D * 2
     shape = (H, D, bs, topk)
@@ -462,16 +478,16 @@ def main():
                             else "pool, select, forward in sequence on one stream")},
         "ms_select": t_sel, "ms_fwd": t_fwd,
         "fwd_gather_GBps_effective": gathered / (t_fwd * 1e-3) / 1e9,
-        # HBM bytes actually moved per forward launch (rocprofv3 FETCH_SIZE + WRITE_SIZE,
-        # copy-calibrated) over the launch time, against the 8 TB/s peak
-        "fwd_hbm_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
-        "fwd_hbm_frac_of_peak": (traffic_b / (t_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS) if traffic_b else None,
+        # bytes the L2s exchange with the fabric per forward launch (rocprofv3 FETCH_SIZE +
+        # WRITE_SIZE, copy-calibrated: L2 misses, Infinity Cache hits included) over the
+        # launch time, against the 8 TB/s HBM peak
+        "fwd_l2miss_GBps": (traffic_b / (t_fwd * 1e-3) / 1e9) if traffic_b else None,
+        "fwd_l2miss_frac_of_hbm_peak": (traffic_b / (t_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS) if traffic_b else None,
         # the selection's algorithmic bytes (q and k read once by the pooling) over its time
         "select_hbm_GBps_algorithmic": (2 * B * H * N * D * 2) / (t_sel * 1e-3) / 1e9,
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS,
-                     "traffic": traffic_b, "traffic_source": traffic_note,
-                     "kernel": "fbsa::fwd_kernel<bf16,64,64>", "flop_per_launch": flops},
+        # compulsory bytes: q, k, v read and o written once (+ the selection list)
+        "roofline": roofline_record(flops, 4 * B * H * N * D * 2 + B * nblk * kk * 4, t_fwd,
+                                    f"fbsa::fwd_kernel<bf16,{bs},{D}>", traffic_b, traffic_note),
         "strict_roofline_select_fwd_us": None,
     }
     # strict roofline of the whole select+fwd step: selection reads q,k once (HBM), forward FLOPs (MFMA)
@@ -496,13 +512,13 @@ def main():
         # the forward's 2 (S, dP, dV, dQ, dK) = 2.5x the forward's FLOPs; this build
         # recomputes S and dP in both the dQ and the dK/dV kernel (3.5x)
         bflops = 2.5 * flops
-        bach = bflops / (t_bwd * 1e-3) / 1e12
         out["ms_bwd"] = t_bwd
         out["bwd"] = {"ms": t_bwd, "tokens_per_s": B * N / (t_bwd * 1e-3),
-                      "roofline": {"bound": "mfma", "achieved": bach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                   "frac": bach / PEAK_BF16_TFLOPS, "flop_per_launch": bflops,
-                                   "implementation_flop_per_launch": 3.5 * flops,
-                                   "t_star_us": bflops / (PEAK_BF16_TFLOPS * 1e12) * 1e6},
+                      # compulsory bytes: q, k, v, o, dO read, dq, dk, dv written once
+                      "roofline": dict(roofline_record(bflops, 8 * B * H * N * D * 2, t_bwd, "backward (all stages)"),
+                                       implementation_flop_per_launch=3.5 * flops,
+                                       t_star_us=max(bflops / (PEAK_BF16_TFLOPS * 1e12),
+                                                     8 * B * H * N * D * 2 / (PEAK_HBM_GBS * 1e9)) * 1e6),
                       "stages": "prep (delta, lse), transposed index (stable radix sort), dQ, dK/dV"}
         out["ms_select_fwd_bwd"] = ms_step + t_bwd
         out["train_step_tokens_per_s"] = B * N / ((ms_step + t_bwd) * 1e-3)

@@ -3,7 +3,9 @@
 #include <stdio.h>
 #include <math.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "fbsa_common.h"
 #include "fbsa_internal.h"
@@ -24,6 +26,24 @@ int hip_check(hipError_t e, const char *what) {
   if (e == hipSuccess) return FBSA_OK;
   (void)hipGetLastError();  // clear the sticky per-thread error so later calls are not blamed
   return fail(FBSA_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int lds_optin(const void *fn, size_t bytes, const char *what) {
+  if (bytes <= 64 * 1024) return FBSA_OK;
+  int dev = 0;
+  int e = hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (e) return e;
+  // grants per (device, kernel); a mutex because autograd runs the backward on
+  // its own device thread while other host threads may launch
+  static std::mutex mu;
+  static std::map<std::pair<int, const void *>, size_t> granted;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t &g = granted[std::make_pair(dev, fn)];
+  if (bytes <= g) return FBSA_OK;
+  e = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes), what);
+  if (e) return e;
+  g = bytes;
+  return FBSA_OK;
 }
 
 static int64_t esize(int dtype) { return dtype == FBSA_F32 ? 4 : 2; }

@@ -143,9 +143,10 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   lay->vals_out = off; off = al256(off + (size_t)lay->n * 4);
   lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
   lay->sort_tmp = off; off = al256(off + tmp);
-  // dK/dV list segments of at most ~4096 chunks per workgroup (512 for fp32
-  // operands: a segment's fp32 accumulator then sums 8x fewer rows, which keeps
-  // the rounding of sums over ~1e5 query rows under 1e-4 of the result's scale)
+  // dK/dV list segments of at most FBSA_SEG_CHUNKS (512) work chunks per
+  // workgroup for every dtype: a segment's fp32 accumulator then sums at most
+  // 512 chunks of query rows, which keeps the rounding of sums over ~1e5 query
+  // rows under 1e-4 of the result's scale (fp32) and shortens the longest walk
   const int64_t grp = d->Hq / d->Hkv;
   const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
   int64_t segE = (d->dtype == FBSA_F32 ? 512 : FBSA_SEG_CHUNKS) / (grp * (d->bs / kc));
@@ -1260,22 +1261,15 @@ static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, Bw
   if (a.dense) a.ent = nullptr;
 }
 
-template <typename K> static int set_lds(K kern, size_t lds, size_t &granted, const char *what) {
+template <typename K> static int set_lds(K kern, size_t lds, const char *what) {
   if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "%s needs %zu bytes of LDS", what, lds);
-  if (lds > 64 * 1024 && lds > granted) {
-    int e = hip_check(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                      "hipFuncSetAttribute(bwd)");
-    if (e) return e;
-    granted = lds;
-  }
-  return FBSA_OK;
+  return lds_optin((const void *)kern, lds, "hipFuncSetAttribute(bwd)");
 }
 
 template <typename T, int BS, int D, bool DENSE> static int launch_dq_as(const BwdArgs &a, hipStream_t s) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
-  static size_t granted = 0;
-  int e = set_lds(dq_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dq");
+  int e = set_lds(dq_kernel<T, BS, D, DENSE>, lds, "fbsa_bwd_dq");
   if (e) return e;
   hipLaunchKernelGGL((dq_kernel<T, BS, D, DENSE>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dq_kernel launch");
@@ -1288,8 +1282,7 @@ template <typename T, int BS, int D, bool DENSE> static int launch_dkdv_as(const
                          ? (size_t)(dkdv_pipe<T, BS, D>() ? 2 : 1) * (dkdv_keys<T, BS, D>() / 16) * 64 * (HR / 16) * 16
                          : 0;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + 128 * 16 + xch;
-  static size_t granted = 0;
-  int e = set_lds(dkdv_kernel<T, BS, D, DENSE>, lds, granted, "fbsa_bwd_dkdv");
+  int e = set_lds(dkdv_kernel<T, BS, D, DENSE>, lds, "fbsa_bwd_dkdv");
   if (e) return e;
   const int64_t nwg = (a.B * a.Hkv * a.nblk + (a.wi_slot ? a.seg_entries_xub : 0)) * (BS / dkdv_keys<T, BS, D>());
   hipLaunchKernelGGL((dkdv_kernel<T, BS, D, DENSE>), dim3((unsigned)nwg), dim3(C::NT), lds, s, a);

@@ -505,15 +505,9 @@ static int launch_fwd_as(const FwdArgs &a, hipStream_t stream) {
   using C = FwdCfg<T, BS, D, QT, KCO, NSO>;
   const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 12);
   if (lds > 160 * 1024 - 64) return fail(FBSA_EUNSUPPORTED, "fbsa_fwd: kk=%lld needs %zu bytes of LDS", (long long)a.kk, lds);
-  if (lds > 64 * 1024) {
-    static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation
-    if (lds > attr_bytes) {
-      int e = hip_check(hipFuncSetAttribute((const void *)fwd_kernel<T, BS, D, QT, KCO, NSO, DENSE>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                        "hipFuncSetAttribute(fwd)");
-      if (e) return e;
-      attr_bytes = lds;
-    }
+  {
+    const int e = lds_optin((const void *)fwd_kernel<T, BS, D, QT, KCO, NSO, DENSE>, lds, "hipFuncSetAttribute(fwd)");
+    if (e) return e;
   }
   const int64_t nwg = a.B * a.Hq * a.ni;
   if (nwg == 0) return FBSA_OK;

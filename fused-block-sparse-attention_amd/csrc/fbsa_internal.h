@@ -29,6 +29,11 @@ struct FwdArgs {
 constexpr int64_t kSelListMax = 62;
 constexpr int64_t kSelWideMax = 4096;
 
+// Opts kernel `fn` into `bytes` of dynamic LDS on the current device (needed
+// above 64 KiB). Thread-safe; the grant is remembered per (device, kernel), so
+// the attribute is set once per device and size increase.
+int lds_optin(const void *fn, size_t bytes, const char *what);
+
 int run_fwd(const fbsa_attn_desc *d, const FwdArgs &a, hipStream_t s);
 int run_pool(const fbsa_pool_desc *d, const void *x, void *out, void *out2, hipStream_t s);
 int run_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk, const void *k,

@@ -193,19 +193,10 @@ __global__ __launch_bounds__(BS * 4) void mass_kernel(MassArgs a) {
 template <typename T, int BS, int D> static int launch_mass(const MassArgs &a, hipStream_t s) {
   using C = MassCfg<T, BS, D>;
   const size_t lds = (size_t)C::NSTAGE * C::TILE_BYTES + 2 * C::NW * sizeof(float);
-  if (lds > 64 * 1024) {
-    static size_t granted = 0;
-    if (lds > granted) {
-      int e = hip_check(hipFuncSetAttribute((const void *)mass_kernel<T, BS, D, 1>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                        "hipFuncSetAttribute(mass)");
-      if (!e)
-        e = hip_check(hipFuncSetAttribute((const void *)mass_kernel<T, BS, D, 2>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                      "hipFuncSetAttribute(mass)");
-      if (e) return e;
-      granted = lds;
-    }
+  {
+    int e = lds_optin((const void *)mass_kernel<T, BS, D, 1>, lds, "hipFuncSetAttribute(mass)");
+    if (!e) e = lds_optin((const void *)mass_kernel<T, BS, D, 2>, lds, "hipFuncSetAttribute(mass)");
+    if (e) return e;
   }
   const unsigned nwg = (unsigned)(a.B * a.Hq * a.nblk);
   hipLaunchKernelGGL((mass_kernel<T, BS, D, 1>), dim3(nwg), dim3(C::NT), lds, s, a);

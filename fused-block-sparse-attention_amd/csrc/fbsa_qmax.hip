@@ -644,15 +644,9 @@ __global__ __launch_bounds__(256) void qm_norms_kernel(QmaxArgs a) {
 
 template <typename T, int D, int TOK> static int launch_qmax_k(const QmaxArgs &a, hipStream_t s) {
   const size_t lds = qm_lds_bytes<D, TOK>(a.ncolp);
-  if (lds > 64 * 1024) {
-    static size_t attr_bytes = 0;  // largest opt-in granted so far for this instantiation
-    if (lds > attr_bytes) {
-      int e = hip_check(hipFuncSetAttribute((const void *)qmax_kernel<T, D, TOK>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                        "hipFuncSetAttribute(qmax)");
-      if (e) return e;
-      attr_bytes = lds;
-    }
+  {
+    const int e = lds_optin((const void *)qmax_kernel<T, D, TOK>, lds, "hipFuncSetAttribute(qmax)");
+    if (e) return e;
   }
   hipLaunchKernelGGL((qmax_kernel<T, D, TOK>), dim3((unsigned)(a.B * a.H * a.nblk)), dim3(256), lds, s, a);
   return FBSA_OK;

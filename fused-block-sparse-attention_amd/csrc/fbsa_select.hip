@@ -1724,13 +1724,9 @@ template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, v
     int KP = 256;
     while (KP < K) KP <<= 1;
     const size_t lds = (size_t)2 * KP * 8 + (size_t)2 * D * 8 + (size_t)(KP + 2) * 4;
-    static size_t granted = 0;
-    if (lds > 64 * 1024 && lds > granted) {
-      int e = hip_check(hipFuncSetAttribute((const void *)select_wide_kernel<T, D, MODE>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
-                        "hipFuncSetAttribute(select_wide)");
+    {
+      const int e = lds_optin((const void *)select_wide_kernel<T, D, MODE>, lds, "hipFuncSetAttribute(select_wide)");
       if (e) return e;
-      granted = lds;
     }
     const int64_t nwg = (a.row1 - a.row0) * a.B * a.H;
     hipLaunchKernelGGL((select_wide_kernel<T, D, MODE>), dim3((unsigned)nwg), dim3(256), lds, s, a, KP);
