@@ -60,6 +60,11 @@ def parse():
     p.add_argument("--cpu-rows", type=int, default=4096, help="query blocks in the CPU sample (4096 = all at config 3)")
     p.add_argument("--qwen", choices=["max", "qmax", "twostage", "lasttok"], default=None,
                    help="time configuration 4 instead (GQA Qwen shape) with this qwen_blocksparse selector")
+    p.add_argument("--sweep", action="store_true",
+                   help="selection-vs-read crossover sweep (src/bench_crossover.py): one JSON line per "
+                        "(block, L) point, then the fitted scaling exponents")
+    p.add_argument("--sweep-lengths", default="262144,1048576,4194304,16777216")
+    p.add_argument("--sweep-blocks", default="32,64,128")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy 3 times (HBM counter calibration)")
     return p.parse_args()
@@ -384,6 +389,92 @@ class _Fixed:
         return self.idx
 
 
+def crossover_sweep(a):
+    """Selection and attention read timed separately over context lengths and
+    block sizes, as src/bench_crossover.py:97-153 does: D_model 512, H 8,
+    dh 64, top-8 (kk 9), sel_dim 32, causal, bf16, B 1. Selection is the
+    BlockSparseSSA module's own stage (MLP selector features pooled per block,
+    then the max-of-two-products convention-A top-k on the streaming kernel;
+    no nblk x nblk matrix); the read is the fused forward on a fabricated
+    causal selection (own block + 8 uniform random blocks, future ones masked)
+    with a log-sigmoid gate bias, as make_sel / bsattn_forward there. Times
+    are wall clock around synchronised iterations (warm-up 2 / iterations 5
+    up to 1M tokens, 1 / 3 beyond), peak memory from torch's allocator."""
+    import math
+    import torch
+    import torch.nn.functional as F
+    from fbsa_amd import ops
+    from ssa_model import BlockSparseSSA
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    Dm, H, topk, sel_dim, B = 512, 8, 8, 32, 1
+    dh = Dm // H
+    kk = topk + 1
+    lengths = [int(x) for x in a.sweep_lengths.split(",")]
+    blocks = [int(x) for x in a.sweep_blocks.split(",")]
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def timed(fn, iters, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / iters * 1e3, torch.cuda.max_memory_allocated() / 1e9
+
+    pts = []
+    for bs in blocks:
+        for L in lengths:
+            nblk = L // bs
+            iters, warmup = (5, 2) if L <= 1048576 else (3, 1)
+            model = BlockSparseSSA(Dm, H, block=bs, topk=topk, sel_dim=sel_dim, causal=True,
+                                   use_triton=True).to(dev).to(torch.bfloat16).eval()
+            x = torch.randn(B, L, Dm, generator=g, device=dev, dtype=torch.bfloat16)
+
+            def select():
+                sq, sk_mean, sk_max = model._pooled(x, B, nblk, bs)
+                return model._select(sq, sk_mean, sk_max)
+
+            with torch.no_grad():
+                sel_ms, sel_gb = timed(select, iters, warmup)
+            del x, model
+            torch.cuda.empty_cache()
+            q, k, v = (torch.randn(B, H, L, dh, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(3))
+            own = torch.arange(nblk, device=dev).view(1, nblk, 1)
+            rnd = torch.randint(0, nblk, (B, nblk, kk - 1), generator=g, device=dev)
+            sel = torch.cat([own.expand(B, nblk, 1), rnd], -1).to(torch.int32)[:, None]
+            gate = F.logsigmoid(torch.randn(B, 1, nblk, kk, generator=g, device=dev))
+            with torch.no_grad():
+                attn_ms, attn_gb = timed(lambda: ops.attention_forward(q, k, v, sel, mask=ops.MASK_SLOT_CAUSAL,
+                                                                       gate=gate), iters, warmup)
+            del q, k, v, sel, gate
+            torch.cuda.empty_cache()
+            pt = {"sweep": "crossover", "block": bs, "L": L, "nblk": nblk, "sel_ms": sel_ms, "attn_ms": attn_ms,
+                  "sel_GB": sel_gb, "attn_GB": attn_gb,
+                  # the reference's analytical FLOPs (src/bench_crossover.py:104-105)
+                  "sel_pflop": 2 * 2 * B * nblk * nblk * sel_dim / 1e15,
+                  "attn_pflop": 2 * 2 * B * H * L * kk * bs * dh / 1e15}
+            pts.append(pt)
+            print(json.dumps(pt), flush=True)
+
+    def slope(xs, ys):
+        lx, ly = [math.log(x) for x in xs], [math.log(y) for y in ys]
+        mx, my = sum(lx) / len(lx), sum(ly) / len(ly)
+        return sum((u - mx) * (w - my) for u, w in zip(lx, ly)) / sum((u - mx) ** 2 for u in lx)
+
+    fit = {}
+    for bs in blocks:
+        ps = [p for p in pts if p["block"] == bs]
+        if len(ps) >= 2:
+            fit[str(bs)] = {"sel_exponent": slope([p["L"] for p in ps], [p["sel_ms"] for p in ps]),
+                            "attn_exponent": slope([p["L"] for p in ps], [p["attn_ms"] for p in ps])}
+    print(json.dumps({"sweep": "crossover_fit", "loglog_slope_vs_L": fit}), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -392,6 +483,9 @@ def main():
         sys.exit(2)
     if a.calibrate_copy:
         calibrate_copy()
+        return
+    if a.sweep:
+        crossover_sweep(a)
         return
     if a.qwen:
         qwen_main(a)

@@ -77,6 +77,12 @@ static int check_attn(const fbsa_attn_desc *d, const char *fn) {
       if (st[t][x] < 0 || (st[t][x] * es) % 16)
         return fail(FBSA_EINVAL, "%s: %s stride[%d]=%lld must be a non-negative multiple of 16 bytes", fn, nm[t], x,
                     (long long)st[t][x]);
+  // the kernels form row offsets as 32 x 32 -> 64-bit products
+  if (d->L >= 0x80000000LL) return fail(FBSA_EUNSUPPORTED, "%s: L=%lld must be below 2^31", fn, (long long)d->L);
+  const int64_t rs[5] = {d->sq[2], d->sk[2], d->sv[2], d->so[2], d->sdo[2]};
+  for (int t = 0; t < 5; ++t)
+    if (rs[t] * es >= 0x100000000LL)
+      return fail(FBSA_EUNSUPPORTED, "%s: a row stride of %lld elements is 4 GiB or more", fn, (long long)rs[t]);
   return FBSA_OK;
 }
 
@@ -319,7 +325,7 @@ namespace fbsa {
 static int check_bwd(const fbsa_attn_desc *d, const char *fn, BwdLayout *lay, const void *ws, size_t ws_bytes) {
   int e = check_attn(d, fn);
   if (e) return e;
-  if (d->flags & ~(FBSA_FLAG_OUT_GATE | FBSA_FLAG_DENSE)) return fail(FBSA_EINVAL, "%s: unknown flags 0x%x", fn, d->flags);
+  if (d->flags & ~(FBSA_FLAG_OUT_GATE | FBSA_FLAG_DENSE | FBSA_FLAG_DGATE)) return fail(FBSA_EINVAL, "%s: unknown flags 0x%x", fn, d->flags);
   if ((d->flags & FBSA_FLAG_DENSE) && (e = check_dense(d, nullptr, nullptr, fn))) return e;
   e = bwd_layout(d, lay);
   if (e) return e;
@@ -395,6 +401,9 @@ int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const voi
   if (e) return e;
   if ((e = check_dense(d, sel, gate, "fbsa_bwd_dq"))) return e;
   if ((d->flags & FBSA_FLAG_DENSE) && dgate) return fail(FBSA_EINVAL, "fbsa_bwd_dq: FBSA_FLAG_DENSE has no gate gradient");
+  if (dgate && d->dtype != FBSA_F32 && !(d->flags & FBSA_FLAG_DGATE))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dq: a 16-bit gate gradient needs FBSA_FLAG_DGATE in the descriptor "
+                             "(the workspace then holds the per-row slot masses)");
   if ((sel && !aligned(sel, 4)) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
     return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned");
   if (!dq || !aligned(dq, 16)) return fail(FBSA_EINVAL, "fbsa_bwd_dq: dq must be non-null and 16-byte aligned");

@@ -62,6 +62,30 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_BWD_TRWIN
 #define FBSA_BWD_TRWIN 8
 #endif
+// 16-bit types: P and dS enter the dK and dV products as hi/lo operand pairs
+// (two MFMAs each) for key blocks read by more than FBSA_BWD_SPLIT_ROWS query
+// rows (list entries x GQA group x block rows), so long fp32 sums over a key
+// block's readers carry no per-term 16-bit rounding of P or dS
+#ifndef FBSA_BWD_SPLIT
+#define FBSA_BWD_SPLIT 1
+#endif
+#ifndef FBSA_BWD_SPLIT_ROWS
+#define FBSA_BWD_SPLIT_ROWS 16384
+#endif
+
+// dQ with 16-bit operands: the row's delta is recomputed as sum P dP over its
+// keys (fp32, from the unrounded P), replacing the prep's sum dO O (which
+// reads the 16-bit O, formed from 16-bit P); dQ is then corrected by
+// -(delta - delta_prep) sum P K from a second product on the same K reads
+// (head dims up to FBSA_DQ_CORR_DMAX: at d 256 its accumulators do not fit the
+// register budget), and dS enters the dQ product as a hi/lo pair when
+// FBSA_DQ_SPLIT is set
+#ifndef FBSA_DQ_CORR_DMAX
+#define FBSA_DQ_CORR_DMAX 0
+#endif
+#ifndef FBSA_DQ_SPLIT
+#define FBSA_DQ_SPLIT 0
+#endif
 
 // extra list segments: a segment's workgroups placed on one XCD
 #ifndef FBSA_XSEG_XCD
@@ -91,6 +115,42 @@ __host__ __device__ inline int64_t dense_prefix(int64_t j, int64_t nblk, int64_t
   return causal ? m * nblk - m * (m - 1) / 2 : m * nblk;
 }
 
+// dK/dV list segments of at most FBSA_SEG_CHUNKS (512) work chunks per
+// workgroup: a segment's fp32 accumulator then sums at most 512 chunks of
+// query rows, which keeps the rounding of sums over ~1e5 query rows under 1e-4
+// of the result's scale (fp32) and shortens the longest walk. `maxlist` is the
+// longest possible list, `walked` the (list entry, KV head) pairs in all.
+static int seg_layout(const fbsa_attn_desc *d, BwdLayout *lay, int64_t maxlist, int64_t walked, size_t &off) {
+  const int64_t grp = d->Hq / d->Hkv;
+  const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
+  int64_t segE = (d->dtype == FBSA_F32 ? 512 : FBSA_SEG_CHUNKS) / (grp * (d->bs / kc));
+  if (segE < 16) segE = 16;
+  lay->nwi = d->B * d->Hkv * d->nblk;
+  if (lay->nwi >= 0x7fffffffLL)
+    return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: B * Hkv * nblk too large for the 32-bit list segments");
+  lay->seg_entries = maxlist > segE ? segE : 0;
+  lay->xub = lay->slots_ub = 0;
+  lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
+  lay->scan_tmp_bytes = 0;
+  if (lay->seg_entries) {
+    lay->xub = walked / segE + 1;
+    lay->slots_ub = 2 * (walked / segE) + 1;
+    size_t stmp = 0;
+    hipError_t e = rocprim::exclusive_scan(nullptr, stmp, (const uint64_t *)nullptr, (uint64_t *)nullptr,
+                                           (uint64_t)0, (size_t)(lay->nwi + 1), rocprim::plus<uint64_t>(),
+                                           (hipStream_t)0);
+    if (e != hipSuccess) return hip_check(e, "scan workspace query");
+    lay->scan_tmp_bytes = stmp;
+    lay->seg_cnt = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
+    lay->seg_pos = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
+    lay->wi_slot = off; off = al256(off + (size_t)lay->nwi * 4);
+    lay->xtab = off; off = al256(off + (size_t)lay->xub * 16);
+    lay->partials = off; off = al256(off + (size_t)lay->slots_ub * 2 * (size_t)(d->bs * d->D) * 4);
+    lay->scan_tmp = off; off = al256(off + stmp);
+  }
+  return FBSA_OK;
+}
+
 int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   const bool dense = (d->flags & FBSA_FLAG_DENSE) != 0;
   lay->nseg = d->B * d->hsel * d->nblk;
@@ -109,13 +169,16 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
     lay->rowstat = off; off = al256(off + rows * 8);
     lay->dout_attn = off;
     if (d->flags & FBSA_FLAG_OUT_GATE) off = al256(off + rows * (size_t)d->D * (size_t)esize(d->dtype));
-    lay->dgate_part = lay->keys_in = lay->keys_out = lay->vals_in = lay->vals_out = off;
+    lay->dgate_part = lay->pmass = lay->keys_in = lay->keys_out = lay->vals_in = lay->vals_out = off;
     lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
     lay->sort_tmp = off;
-    lay->nwi = d->B * d->Hkv * d->nblk;
-    lay->seg_entries = lay->xub = lay->slots_ub = 0;  // lists are long for every block: no segments
-    lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
-    lay->scan_tmp_bytes = 0;
+    // fp32: every list longer than a segment is walked in segments, as for an
+    // explicit list (closed-form offsets); 16-bit types walk each list whole
+    // (their long sums take hi/lo operands; segments of every list would need
+    // fp32 partials of about the size of the whole dense gradient)
+    const int64_t maxlist = d->dtype == FBSA_F32 ? d->nblk : 0;
+    int e = seg_layout(d, lay, maxlist, per * d->B * d->Hkv, off);
+    if (e) return e;
     lay->total = off;
     return FBSA_OK;
   }
@@ -137,46 +200,19 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
   lay->dout_attn = off;
   if (d->flags & FBSA_FLAG_OUT_GATE) off = al256(off + rows * (size_t)d->D * (size_t)esize(d->dtype));
   lay->dgate_part = off; off = al256(off + (size_t)(d->B * d->Hq * d->nblk * d->kk) * 4);
+  lay->pmass = off;
+  if ((d->flags & FBSA_FLAG_DGATE) && d->dtype != FBSA_F32) off = al256(off + (size_t)(d->B * d->Hq * d->L * d->kk) * 4);
   lay->keys_in = off; off = al256(off + (size_t)lay->n * 4);
   lay->keys_out = off; off = al256(off + (size_t)lay->n * 4);
   lay->vals_in = off; off = al256(off + (size_t)lay->n * 4);
   lay->vals_out = off; off = al256(off + (size_t)lay->n * 4);
   lay->seg_off = off; off = al256(off + (size_t)(lay->nseg + 1) * 4);
   lay->sort_tmp = off; off = al256(off + tmp);
-  // dK/dV list segments of at most FBSA_SEG_CHUNKS (512) work chunks per
-  // workgroup for every dtype: a segment's fp32 accumulator then sums at most
-  // 512 chunks of query rows, which keeps the rounding of sums over ~1e5 query
-  // rows under 1e-4 of the result's scale (fp32) and shortens the longest walk
-  const int64_t grp = d->Hq / d->Hkv;
-  const int64_t kc = d->bs < (d->D >= 256 ? 32 : 64) ? d->bs : (d->D >= 256 ? 32 : 64);
-  int64_t segE = (d->dtype == FBSA_F32 ? 512 : FBSA_SEG_CHUNKS) / (grp * (d->bs / kc));
-  if (segE < 16) segE = 16;
-  lay->nwi = d->B * d->Hkv * d->nblk;
-  if (lay->nwi >= 0x7fffffffLL)
-    return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: B * Hkv * nblk too large for the 32-bit list segments");
   // the longest possible list: token-causal selections are deduplicated, the
   // other masks count a block chosen in several slots of a row once per slot
   const int64_t maxlist = d->mask == FBSA_MASK_TOKEN_CAUSAL ? d->nblk : d->nblk * d->kk;
-  lay->seg_entries = maxlist > segE ? segE : 0;
-  lay->xub = lay->slots_ub = 0;
-  lay->seg_cnt = lay->seg_pos = lay->wi_slot = lay->xtab = lay->partials = lay->scan_tmp = off;
-  lay->scan_tmp_bytes = 0;
-  if (lay->seg_entries) {
-    const int64_t walked = lay->n * (d->Hkv / d->hsel);  // hsel is 1 or Hkv
-    lay->xub = walked / segE + 1;
-    lay->slots_ub = 2 * (walked / segE) + 1;
-    size_t stmp = 0;
-    e = rocprim::exclusive_scan(nullptr, stmp, (const uint64_t *)nullptr, (uint64_t *)nullptr, (uint64_t)0,
-                                (size_t)(lay->nwi + 1), rocprim::plus<uint64_t>(), (hipStream_t)0);
-    if (e != hipSuccess) return hip_check(e, "scan workspace query");
-    lay->scan_tmp_bytes = stmp;
-    lay->seg_cnt = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
-    lay->seg_pos = off; off = al256(off + (size_t)(lay->nwi + 1) * 8);
-    lay->wi_slot = off; off = al256(off + (size_t)lay->nwi * 4);
-    lay->xtab = off; off = al256(off + (size_t)lay->xub * 16);
-    lay->partials = off; off = al256(off + (size_t)lay->slots_ub * 2 * (size_t)(d->bs * d->D) * 4);
-    lay->scan_tmp = off; off = al256(off + stmp);
-  }
+  int e2 = seg_layout(d, lay, maxlist, lay->n * (d->Hkv / d->hsel), off);  // hsel is 1 or Hkv
+  if (e2) return e2;
   lay->total = off;
   return FBSA_OK;
 }
@@ -407,11 +443,12 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 // ----------------------------------------------------------------- stages 3, 4
 struct BwdArgs {
   const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
-  const float2 *rowstat;
+  float2 *rowstat;  // (lse * log2 e, delta); dq_kernel replaces delta by sum P dP (16-bit types)
   const int32_t *sel;
   const float *gate;
   void *dq, *dk, *dv;
   float *dgate_part;
+  float *pmass;  // 16-bit gate gradient: [b, hq, i][slot][row] probability mass of a row on a slot
   const int32_t *seg_off, *ent;
   const int32_t *wi_slot;  // list segments (null: none): first partial slot of a work item, or -1
   const int4 *xtab;        // extra segments: (work item, first entry, end entry, partial slot)
@@ -446,17 +483,33 @@ template <typename T, int BS, int D, int BUDGET, int META, int ROWS = BS> struct
   static_assert(TILE_BYTES % 1024 == 0, "tile must be whole wave-loads");
 };
 
-template <typename T, int BS, int D, bool DENSE = false>
-__global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
+// bs 64 with 16-bit d <= 64: held to four workgroups per CU (at most 128
+// VGPRs, four waves per SIMD) like the dK/dV kernel; the chunk loop is a short
+// latency-bound chain, so resident waves matter more than registers
+#ifndef FBSA_DQ_MINWG
+#define FBSA_DQ_MINWG 4
+#endif
+template <typename T, int BS, int D> constexpr int dq_minwg() {
+  return (BS == 64 && D <= 64 && sizeof(T) == 2) ? FBSA_DQ_MINWG : 1;
+}
+
+// DG: the gate gradient is asked for (its sums and the slot masses are
+// compiled into the chunk loop only then)
+template <typename T, int BS, int D, bool DENSE = false, bool DG = false>
+__global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdArgs a) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char *stages = smem;
   int *s_blk = (int *)(smem + C::NSTAGE * C::STAGE_BYTES);
   int *s_kind = s_blk + a.kk;
   float *s_gate = (float *)(s_kind + a.kk);
-  int *s_cidx = (int *)(s_gate + a.kk);
-  float *s_dg = (float *)(s_cidx + a.kk);  // [NW][kk], indexed by compact slot
+  int *s_raw = (int *)(s_gate + a.kk);        // DG: the selection slot of each compact slot
+  float *s_dgw = (float *)(s_raw + a.kk);     // DG: [2][NW] per-wave dS sums of the last slot
+  float *s_ddl = s_dgw + 2 * C::NW;           // DG: [BS] per-row delta - delta_prep
   __shared__ int s_nvalid;
+  constexpr bool EXACT = sizeof(T) == 2;
+  constexpr bool CORR = EXACT && D <= FBSA_DQ_CORR_DMAX;
+  constexpr bool DQSPLIT = EXACT && FBSA_DQ_SPLIT;
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
   const int64_t total = a.B * a.Hq * a.nblk;
@@ -496,33 +549,35 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
       }
       const uint64_t m = __ballot(valid);
       const int pos = nout + __popcll(m & ((1ull << lane) - 1ull));
-      if (s < a.kk) s_cidx[s] = valid ? pos : -1;
       if (valid) {
         s_blk[pos] = j;
         s_kind[pos] = kind;
         s_gate[pos] = a.gate ? a.gate[rowoff + s] * kLog2e : 0.f;
+        if (DG) s_raw[pos] = s;
       }
+      // a masked slot's gate gradient is 0
+      if (DG && s < a.kk && !valid) a.dgate_part[((b * a.Hq + hq) * a.nblk + i) * a.kk + s] = 0.f;
       nout += __popcll(m);
     }
     if (lane == 0) s_nvalid = nout;
     if (FBSA_DQ_SORT && nout > 1 && nout <= 64) {
       // ascending key blocks, as the forward walks them; equal blocks keep their
-      // slot order, and the slot -> entry map follows the permutation
-      int j = 0x7fffffff, kind = 0;
+      // slot order (the selection slot of each entry moves with it)
+      int j = 0x7fffffff, kind = 0, rs = 0;
       float gt = 0.f;
-      if (lane < nout) { j = s_blk[lane]; kind = s_kind[lane]; gt = s_gate[lane]; }
+      if (lane < nout) {
+        j = s_blk[lane]; kind = s_kind[lane]; gt = s_gate[lane];
+        if (DG) rs = s_raw[lane];
+      }
       int rank = 0;
       for (int m = 0; m < nout; ++m) {
         const int jm = s_blk[m];
         rank += jm < j || (jm == j && m < lane);
       }
       __builtin_amdgcn_wave_barrier();
-      if (lane < nout) { s_blk[rank] = j; s_kind[rank] = kind; s_gate[rank] = gt; }
-      for (int s0 = 0; s0 < a.kk; s0 += 64) {
-        const int s = s0 + lane;
-        const int c = s < a.kk ? s_cidx[s] : -1;
-        const int rc = __shfl(rank, c < 0 ? 0 : c);
-        if (c >= 0) s_cidx[s] = rc;
+      if (lane < nout) {
+        s_blk[rank] = j; s_kind[rank] = kind; s_gate[rank] = gt;
+        if (DG) s_raw[rank] = rs;
       }
     }
   }
@@ -560,11 +615,17 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
                                    (const char *)(vbase + row0 * a.sv[2]), w);
   };
 
-  f32x4 dqacc[D / 16];
+  f32x4 dqacc[D / 16], bacc[CORR ? D / 16 : 1];  // bacc: sum P K (the delta correction)
 #pragma unroll
   for (int mt = 0; mt < D / 16; ++mt) dqacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float dgl = 0.f;
-  const bool want_dg = a.dgate_part != nullptr;
+#pragma unroll
+  for (int mt = 0; mt < (CORR ? D / 16 : 1); ++mt) bacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dgl = 0.f, pml = 0.f, dacc = 0.f;  // slot's dS sum and P mass; this lane's sum of P dP
+  constexpr bool want_dg = DG;
+  // this workgroup's rows' slot masses ([compact slot][row]; lanes g == 0 of
+  // each wave write and read back their own rows)
+  float *pm = EXACT && want_dg ? a.pmass + ((b * a.Hq + hq) * a.nblk + i) * a.kk * BS : nullptr;
+  float *dgrow = want_dg ? a.dgate_part + ((b * a.Hq + hq) * a.nblk + i) * a.kk : nullptr;
 
 #pragma unroll
   for (int c = 0; c < C::NSTAGE - 1; ++c)
@@ -586,6 +647,13 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     const char *Ks = stages + (c % C::NSTAGE) * C::STAGE_BYTES;
     const char *Vs = Ks + C::TILE_BYTES;
     const int slot = c / C::NCH, ch = c % C::NCH;
+    if (want_dg && ch == 0 && slot > 0 && w == 0) {
+      // the previous slot's per-wave sums are in (written before this barrier)
+      float v = lane < C::NW ? s_dgw[((slot - 1) & 1) * C::NW + lane] : 0.f;
+#pragma unroll
+      for (int x = 1; x < C::NW; x <<= 1) v += shfl_xor_f(v, x);
+      if (lane == 0) dgrow[s_raw[slot - 1]] = v;
+    }
     const int kind = kind_of(slot);
     const float gt = DENSE ? 0.f : s_gate[slot];
     const int64_t j = blk_of(slot);
@@ -595,12 +663,13 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Vs, df, dpacc, g, p);  // dP^T
 
     const float off = gt - lse2;
-    float ds[C::KC / 16][4];
+    float ds[C::KC / 16][4], pp[C::KC / 16][4];
 #pragma unroll
     for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off));
+        pp[m][r] = pv;
         ds[m][r] = pv * (dpacc[m][r] - delta);
       }
     // masked keys (key row 16m + r of the chunk valid iff <= lim): a uniform
@@ -615,21 +684,51 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
       for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (16 * m + r > lim) ds[m][r] = 0.f;
+          if (16 * m + r > lim) { ds[m][r] = 0.f; pp[m][r] = 0.f; }
+    }
+    if constexpr (EXACT) {
+#pragma unroll
+      for (int m = 0; m < C::KC / 16; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dacc = __builtin_fmaf(pp[m][r], dpacc[m][r], dacc);
     }
     if (want_dg) {
 #pragma unroll
       for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dgl += ds[m][r];
+        for (int r = 0; r < 4; ++r) {
+          dgl += ds[m][r];
+          if constexpr (EXACT) pml += pp[m][r];
+        }
     }
     if (want_dg && ch == C::NCH - 1) {
 #pragma unroll
       for (int x = 1; x < 64; x <<= 1) dgl += shfl_xor_f(dgl, x);
-      if (lane == 0) s_dg[w * a.kk + slot] = dgl;
+      if (lane == 0) s_dgw[(slot & 1) * C::NW + w] = dgl;
       dgl = 0.f;
+      if constexpr (EXACT) {
+        // the slot's P mass per query row (its four lanes' parts)
+        pml += shfl_xor_f(pml, 16);
+        pml += shfl_xor_f(pml, 32);
+        if (g == 0) pm[(uint32_t)(slot * BS + tq)] = pml;  // uniform base + 32-bit lane offset
+        pml = 0.f;
+      }
     }
-    mm_tr_acc<T, D, C::KC, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Ks, ds, dqacc, g, p);  // dQ^T += K^T dS^T
+    // dQ^T += K^T dS^T (and, with the delta correction, sum P K from the same reads)
+    if constexpr (CORR)
+      mm_tr_acc<T, D, C::KC, (D >= 128 ? FBSA_BWD_TRWIN : 0), DQSPLIT, 2>(Ks, ds, dqacc, g, p, pp, bacc);
+    else
+      mm_tr_acc<T, D, C::KC, (D >= 128 ? FBSA_BWD_TRWIN : 0), DQSPLIT>(Ks, ds, dqacc, g, p);
+  }
+
+  // the row's delta as sum P dP (its four lanes' parts); dgate and dQ take the
+  // difference to the prep's delta, dK/dV read the new value from the row stats
+  float ddl = 0.f;
+  if constexpr (EXACT) {
+    float dx = dacc + shfl_xor_f(dacc, 16);
+    dx += shfl_xor_f(dx, 32);
+    ddl = dx - delta;
+    if (g == 0) a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = dx;
   }
 
   T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
@@ -642,19 +741,35 @@ __global__ __launch_bounds__(BS * 4) void dq_kernel(BwdArgs a) {
     } else {
       s16x4 pk;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)(dqacc[mt][r] * a.scale));
+      for (int r = 0; r < 4; ++r) {
+        const float y = CORR ? __builtin_fmaf(-ddl, bacc[mt][r], dqacc[mt][r]) : dqacc[mt][r];
+        pk[r] = bits16<T>((T)(y * a.scale));
+      }
       *(s16x4 *)(dqrow + d0) = pk;
     }
   }
   if (want_dg) {
+    // the last slot's sums, and for 16-bit types each slot's correction: minus
+    // the sum over rows of (delta - delta_prep) times the row's P mass on the
+    // slot (wave 0, each lane taking BS / 64 rows)
+    if (EXACT && g == 0) s_ddl[tq] = ddl;
     __syncthreads();
-    float *dst = a.dgate_part + ((b * a.Hq + hq) * a.nblk + i) * a.kk;
-    for (int s = tid; s < a.kk; s += C::NT) {
-      const int ci = s_cidx[s];
-      float v = 0.f;
-      if (ci >= 0)
-        for (int ww = 0; ww < C::NW; ++ww) v += s_dg[ww * a.kk + ci];
-      dst[s] = v;
+    if (w == 0) {
+      if (nv > 0) {
+        float v = lane < C::NW ? s_dgw[((nv - 1) & 1) * C::NW + lane] : 0.f;
+#pragma unroll
+        for (int x = 1; x < C::NW; x <<= 1) v += shfl_xor_f(v, x);
+        if (lane == 0) dgrow[s_raw[nv - 1]] = v;
+      }
+      if constexpr (EXACT) {
+        for (int c = 0; c < nv; ++c) {
+          float v = 0.f;
+          for (int r = lane; r < BS; r += 64) v += pm[(uint32_t)(c * BS + r)] * s_ddl[r];
+#pragma unroll
+          for (int x = 1; x < 64; x <<= 1) v += shfl_xor_f(v, x);
+          if (lane == 0) dgrow[s_raw[c]] -= v;
+        }
+      }
     }
   }
 }
@@ -717,6 +832,7 @@ using DkdvCfg = BwdCfg<T, BS, D,
 template <typename T, int BS, int D, bool DENSE = false>
 __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>())) void dkdv_kernel(BwdArgs a) {
   using C = DkdvCfg<T, BS, D>;
+  constexpr bool SPLIT = FBSA_BWD_SPLIT && sizeof(T) == 2;
   constexpr int ROLES = dkdv_roles<T, D>(), KEYS = dkdv_keys<T, BS, D>();
   constexpr int NPART = BS / KEYS;  // workgroups per key block
   constexpr int MAXE = 128;  // transposed-list entries staged in LDS per batch
@@ -778,6 +894,15 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
     if (a.wi_slot && (slot = a.wi_slot[wi]) >= 0) e1 = e0 + (int)a.seg_entries;
   }
 
+  // hi/lo operands for key blocks whose whole list sums more than
+  // FBSA_BWD_SPLIT_ROWS query rows (a uniform branch): the per-term 16-bit
+  // rounding of P and dS then stays out of long sums, while short lists (most
+  // blocks of a random top-k selection) keep one MFMA per product
+  const bool split = SPLIT && (int64_t)(a.seg_off[seg + 1] - a.seg_off[seg]) * a.grp * BS > FBSA_BWD_SPLIT_ROWS;
+  auto tr_acc = [&](auto SPC, const char *tile, const float (&x)[HR / 16][4], f32x4 *acc) {
+    mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0), decltype(SPC)::value>(tile, x, acc, g, p);
+  };
+
   const int role = ROLES == 2 ? (w & 1) : 0, kw = ROLES == 2 ? (w >> 1) : w;
   const int u = kpart * KEYS + kw * 16 + p;  // this lane's key row within block j (B-operand column)
   const int64_t kpos = j * BS + u;
@@ -812,94 +937,186 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
     tdo[n] = (n * C::NW + w) * 64 >= C::KC * C::CPR;  // == (part != 0), uniform across the wave
   }
 
+  // Q / dO / row-statistics bases of the group's first query head and the
+  // per-head and per-row byte steps
+  const char *qh0 = (const char *)a.q + (b * a.sq[0] + (int64_t)hk * a.grp * a.sq[1]) * C::ES;
+  const char *dh0 = (const char *)a.dout + (b * a.sdo[0] + (int64_t)hk * a.grp * a.sdo[1]) * C::ES;
+  const float2 *rh0 = a.rowstat + (b * a.Hq + (int64_t)hk * a.grp) * a.L;
+  const int64_t qhs = a.sq[1] * C::ES, dhs = a.sdo[1] * C::ES;
+  const uint32_t qrs = (uint32_t)(a.sq[2] * C::ES), drs = (uint32_t)(a.sdo[2] * C::ES);
+
   // dense lists: entry at position e of block j's list is query block dense_i0 + e
   const int64_t dense_i0 = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL ? j : 0) - a.seg_off[seg] : 0;
-  for (int eb = e0; eb < e1; eb += MAXE) {
-    const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
-    __syncthreads();  // the previous batch's entries are no longer read
-    for (int x = tid; x < ne; x += C::NT) {
-      // dense: the list of block j is query blocks j.. (causal) or 0.., slot j
-      int i, s;
-      if (DENSE) {
-        i = (int)(dense_i0 + eb + x);
-        s = (int)j;
-      } else {
-        const uint32_t ev = (uint32_t)a.ent[eb + x];  // i * kk + slot (below 2^31)
-        i = (int)(ev / (uint32_t)a.kk);
-        s = (int)(ev % (uint32_t)a.kk);
-      }
-      int kind = KIND_FULL;
-      if (a.mask == FBSA_MASK_SLOT_CAUSAL) kind = s == 0 ? KIND_DIAG : KIND_FULL;
-      else if (a.mask == FBSA_MASK_NONE) kind = (j + 1) * BS > a.l_valid ? KIND_PAD : KIND_FULL;
-      else if (a.mask == FBSA_MASK_TOKEN_CAUSAL)
-        kind = (j == i || (j + 1) * BS > a.l_valid) ? KIND_ABS : KIND_FULL;
-      const float gt = a.gate ? a.gate[((b * a.hsel + hs) * a.nblk + i) * a.kk + s] * kLog2e : 0.f;
-      s_meta[x] = int4{i, kind, __float_as_int(gt), 0};
-    }
-    __syncthreads();
-    // chunk c = (entry, query head of the group, KC-row chunk), the chunk index fastest;
-    // the issue side and the compute side each step their own counters (no divisions)
-    const int nchunks = ne * a.grp * C::NCH;
-    int ix = 0, ig = 0, ic = 0, istg = 0;  // next chunk to issue and its stage
-    auto issue = [&]() {
-      const int hq = hk * a.grp + ig;
-      const int64_t row0 = (int64_t)s_meta[ix].x * BS + ic * C::KC;
-      const char *qb = (const char *)a.q + (b * a.sq[0] + hq * a.sq[1] + row0 * a.sq[2]) * C::ES;
-      const char *db = (const char *)a.dout + (b * a.sdo[0] + hq * a.sdo[1] + row0 * a.sdo[2]) * C::ES;
-      char *st = stages + istg * C::STAGE_BYTES;
-#pragma unroll
-      for (int n = 0; n < C::LPT; ++n) g2lds16_s(tdo[n] ? db : qb, (unsigned)toff[n], st + (n * C::NW + w) * 1024);
-      // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
-      if (lane < C::KC / (2 * C::NW))
-        g2lds16(a.rowstat + (b * a.Hq + hq) * a.L + row0 + w * (C::KC / C::NW) + 2 * lane,
-                st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
-      if (++ic == C::NCH) {
-        ic = 0;
-        if (++ig == a.grp) { ig = 0; ++ix; }
-      }
-      if (++istg == C::NSTAGE) istg = 0;
-    };
-    if constexpr (dkdv_pipe<T, BS, D>()) {
-      // Two roles, one barrier per chunk. Iteration c: barrier; refill the
-      // stage of chunk c - 2; finish chunk c - 1 (role 0: dV += dO^T P from
-      // its registers; role 1: P from the exchange buffer written before this
-      // barrier, dS, dK += Q^T dS); start chunk c (role 0: S, P into exchange
-      // buffer c & 1; role 1: dP kept in registers). A stage is read in two
-      // iterations, so AHEAD = NSTAGE - 2 chunks are prefetched.
-      static_assert(C::KC == HR && C::NSTAGE >= 3, "one part per chunk, three stages or more");
-      constexpr int AHEAD = C::NSTAGE - 2;
-      constexpr int XS = (KEYS / 16) * 64;  // float4 stride between the parts m of a buffer
-#pragma unroll
-      for (int c = 0; c < AHEAD; ++c)
-        if (c < nchunks) issue();
-      wait_vmcnt<0>();
-      int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
-      float x[HR / 16][4];                   // pending chunk: P (role 0) or dP (role 1)
-      const char *pQ = stages, *pD = stages;
-      const float2 *pM = (const float2 *)stages;
-      for (int c = 0; c <= nchunks; ++c) {
-        if (c < nchunks) {
-          const int ahead = nchunks - 1 - c;
-          wait_ring<C::LPT + 1>(ahead < AHEAD - 1 ? ahead : AHEAD - 1);
+  // the list walk, instantiated with and without the hi/lo operands and with
+  // and without a gate bias (both choices uniform per workgroup and made once,
+  // outside the loops)
+  auto walk = [&](auto SPC, auto GCC) {
+    constexpr bool GC = decltype(GCC)::value;  // gate bias present (else the exponent's offset is -lse)
+    for (int eb = e0; eb < e1; eb += MAXE) {
+      const int ne = e1 - eb < MAXE ? e1 - eb : MAXE;
+      __syncthreads();  // the previous batch's entries are no longer read
+      for (int x = tid; x < ne; x += C::NT) {
+        // dense: the list of block j is query blocks j.. (causal) or 0.., slot j
+        int i, s;
+        if (DENSE) {
+          i = (int)(dense_i0 + eb + x);
+          s = (int)j;
+        } else {
+          const uint32_t ev = (uint32_t)a.ent[eb + x];  // i * kk + slot (below 2^31)
+          i = (int)(ev / (uint32_t)a.kk);
+          s = (int)(ev % (uint32_t)a.kk);
         }
-        lds_barrier();
-        if (c + AHEAD < nchunks) issue();
-        if (c > 0) {
-          if (role == 0) {
-            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(pD, x, dvacc, g, p);  // dV^T += dO^T P
+        int kind = KIND_FULL;
+        if (a.mask == FBSA_MASK_SLOT_CAUSAL) kind = s == 0 ? KIND_DIAG : KIND_FULL;
+        else if (a.mask == FBSA_MASK_NONE) kind = (j + 1) * BS > a.l_valid ? KIND_PAD : KIND_FULL;
+        else if (a.mask == FBSA_MASK_TOKEN_CAUSAL)
+          kind = (j == i || (j + 1) * BS > a.l_valid) ? KIND_ABS : KIND_FULL;
+        const float gt = a.gate ? a.gate[((b * a.hsel + hs) * a.nblk + i) * a.kk + s] * kLog2e : 0.f;
+        s_meta[x] = int4{i, kind, __float_as_int(gt), 0};
+      }
+      __syncthreads();
+      // chunk c = (entry, query head of the group, KC-row chunk), the chunk index fastest;
+      // the issue side and the compute side each step their own counters (no divisions)
+      const int nchunks = ne * a.grp * C::NCH;
+      int ix = 0, ig = 0, ic = 0, istg = 0;  // next chunk to issue and its stage
+      // the current query head's Q, dO and row-statistics bases, stepped when
+      // the head changes; a chunk's rows add a 32 x 32 -> 64-bit product
+      // (row < L < 2^31, row strides below 4 GiB: checked by the host)
+      const char *qh = qh0, *dh = dh0;
+      const float2 *rh = rh0;
+      auto issue = [&]() {
+        const uint32_t row0 = (uint32_t)s_meta[ix].x * (uint32_t)BS + (uint32_t)(ic * C::KC);
+        const char *qb = qh + (uint64_t)row0 * qrs;
+        const char *db = dh + (uint64_t)row0 * drs;
+        char *st = stages + istg * C::STAGE_BYTES;
+  #pragma unroll
+        for (int n = 0; n < C::LPT; ++n) g2lds16_s(tdo[n] ? db : qb, (unsigned)toff[n], st + (n * C::NW + w) * 1024);
+        // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
+        if (lane < C::KC / (2 * C::NW))
+          g2lds16(rh + row0 + w * (C::KC / C::NW) + 2 * lane, st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
+        if (++ic == C::NCH) {
+          ic = 0;
+          if (++ig == a.grp) {
+            ig = 0;
+            ++ix;
+            qh = qh0; dh = dh0; rh = rh0;
           } else {
-            const float4 *xs = s_xch + ((c - 1) & 1) * (HR / 16) * XS + kw * 64 + lane;
-#pragma unroll
-            for (int m = 0; m < HR / 16; ++m) {
-              const float4 pv = xs[m * XS];
-              const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-              for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] - pM[16 * m + 4 * g + r].y);
-            }
-            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(pQ, x, dvacc, g, p);  // dK^T += Q^T dS
+            qh += qhs; dh += dhs; rh += a.L;
           }
         }
-        if (c == nchunks) break;
+        if (++istg == C::NSTAGE) istg = 0;
+      };
+      if constexpr (dkdv_pipe<T, BS, D>()) {
+        // Two roles, one barrier per chunk. Iteration c: barrier; refill the
+        // stage of chunk c - 2; finish chunk c - 1 (role 0: dV += dO^T P from
+        // its registers; role 1: P from the exchange buffer written before this
+        // barrier, dS, dK += Q^T dS); start chunk c (role 0: S, P into exchange
+        // buffer c & 1; role 1: dP kept in registers). A stage is read in two
+        // iterations, so AHEAD = NSTAGE - 2 chunks are prefetched.
+        static_assert(C::KC == HR && C::NSTAGE >= 3, "one part per chunk, three stages or more");
+        constexpr int AHEAD = C::NSTAGE - 2;
+        constexpr int XS = (KEYS / 16) * 64;  // float4 stride between the parts m of a buffer
+  #pragma unroll
+        for (int c = 0; c < AHEAD; ++c)
+          if (c < nchunks) issue();
+        wait_vmcnt<0>();
+        int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
+        float x[HR / 16][4];                   // pending chunk: P (role 0) or dP (role 1)
+        const char *pQ = stages, *pD = stages;
+        const float2 *pM = (const float2 *)stages;
+        for (int c = 0; c <= nchunks; ++c) {
+          if (c < nchunks) {
+            const int ahead = nchunks - 1 - c;
+            wait_ring<C::LPT + 1>(ahead < AHEAD - 1 ? ahead : AHEAD - 1);
+          }
+          lds_barrier();
+          if (c + AHEAD < nchunks) issue();
+          if (c > 0) {
+            if (role == 0) {
+              tr_acc(SPC, pD, x, dvacc);  // dV^T += dO^T P
+            } else {
+              const float4 *xs = s_xch + ((c - 1) & 1) * (HR / 16) * XS + kw * 64 + lane;
+  #pragma unroll
+              for (int m = 0; m < HR / 16; ++m) {
+                const float4 pv = xs[m * XS];
+                const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+  #pragma unroll
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] - pM[16 * m + 4 * g + r].y);
+              }
+              tr_acc(SPC, pQ, x, dvacc);  // dK^T += Q^T dS
+            }
+          }
+          if (c == nchunks) break;
+
+          const char *Qs = stages + cstg * C::STAGE_BYTES;
+          const char *Ds = Qs + C::TILE_BYTES;
+          const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
+          const int4 meta = s_meta[cx];
+          const int ch = cch;
+          const int kind = meta.y;
+          const float gt = __int_as_float(meta.z);
+          const int64_t i = meta.x;
+          if (++cch == C::NCH) {
+            cch = 0;
+            if (++cg == a.grp) { cg = 0; ++cx; }
+          }
+          if (++cstg == C::NSTAGE) cstg = 0;
+          int tmin = -(1 << 30);
+          bool kok = true;
+          if (kind == KIND_DIAG) tmin = u;
+          else if (kind == KIND_PAD) kok = keyok;
+          else if (kind == KIND_ABS) {
+            const int64_t tm = (int64_t)u - (i - j) * BS;
+            tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);
+            kok = keyok;
+          }
+          tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
+
+          f32x4 xacc[HR / 16];
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Ds : Qs, kf, xacc, g, p);  // S or dP
+          if (role == 0) {
+            float4 *xs = s_xch + (c & 1) * (HR / 16) * XS + kw * 64 + lane;
+  #pragma unroll
+            for (int m = 0; m < HR / 16; ++m) {
+  #pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float2 ms = Ms[16 * m + 4 * g + r];
+                const bool ok = kok && (16 * m + r >= tmin);
+                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                asm volatile("" : "+v"(ev));
+                x[m][r] = ok ? ev : 0.f;
+              }
+              xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
+            }
+          } else {
+  #pragma unroll
+            for (int m = 0; m < HR / 16; ++m)
+  #pragma unroll
+              for (int r = 0; r < 4; ++r) x[m][r] = xacc[m][r];
+          }
+          pQ = Qs; pD = Ds; pM = Ms;
+        }
+        continue;
+      }
+
+  #pragma unroll
+      for (int c = 0; c < C::NSTAGE - 1; ++c)
+        if (c < nchunks) issue();
+      // the register-operand loads above and the first stages have landed (issued
+      // together, so their latencies overlap): the compiler then waits for nothing
+      // inside the ring loop, where its own waits would also drain the prefetch
+      wait_vmcnt<0>();
+
+
+      int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
+      for (int c = 0; c < nchunks; ++c) {
+        // stage c has landed for this wave (LPT + 1 loads per stage; up to NSTAGE - 2 later
+        // stages may still be in flight); after the barrier every wave's part has landed and
+        // every wave is done with chunk c - 1, whose stage the refill below overwrites
+        const int ahead = nchunks - 1 - c;
+        wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
+        lds_barrier();
+        if (c + C::NSTAGE - 1 < nchunks) issue();
 
         const char *Qs = stages + cstg * C::STAGE_BYTES;
         const char *Ds = Qs + C::TILE_BYTES;
@@ -914,6 +1131,8 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
           if (++cg == a.grp) { cg = 0; ++cx; }
         }
         if (++cstg == C::NSTAGE) cstg = 0;
+
+        // valid iff query row (within block i) >= tmin, and the key is in range
         int tmin = -(1 << 30);
         bool kok = true;
         if (kind == KIND_DIAG) tmin = u;
@@ -925,151 +1144,90 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         }
         tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
 
-        f32x4 xacc[HR / 16];
-        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Ds : Qs, kf, xacc, g, p);  // S or dP
-        if (role == 0) {
-          float4 *xs = s_xch + (c & 1) * (HR / 16) * XS + kw * 64 + lane;
-#pragma unroll
-          for (int m = 0; m < HR / 16; ++m) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float2 ms = Ms[16 * m + 4 * g + r];
-              const bool ok = kok && (16 * m + r >= tmin);
-              float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, gt - ms.x));
-              asm volatile("" : "+v"(ev));
-              x[m][r] = ok ? ev : 0.f;
-            }
-            xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
-          }
-        } else {
-#pragma unroll
-          for (int m = 0; m < HR / 16; ++m)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x[m][r] = xacc[m][r];
-        }
-        pQ = Qs; pD = Ds; pM = Ms;
-      }
-      continue;
-    }
-
-#pragma unroll
-    for (int c = 0; c < C::NSTAGE - 1; ++c)
-      if (c < nchunks) issue();
-    // the register-operand loads above and the first stages have landed (issued
-    // together, so their latencies overlap): the compiler then waits for nothing
-    // inside the ring loop, where its own waits would also drain the prefetch
-    wait_vmcnt<0>();
-
-
-    int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
-    for (int c = 0; c < nchunks; ++c) {
-      // stage c has landed for this wave (LPT + 1 loads per stage; up to NSTAGE - 2 later
-      // stages may still be in flight); after the barrier every wave's part has landed and
-      // every wave is done with chunk c - 1, whose stage the refill below overwrites
-      const int ahead = nchunks - 1 - c;
-      wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
-      lds_barrier();
-      if (c + C::NSTAGE - 1 < nchunks) issue();
-
-      const char *Qs = stages + cstg * C::STAGE_BYTES;
-      const char *Ds = Qs + C::TILE_BYTES;
-      const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
-      const int4 meta = s_meta[cx];
-      const int ch = cch;
-      const int kind = meta.y;
-      const float gt = __int_as_float(meta.z);
-      const int64_t i = meta.x;
-      if (++cch == C::NCH) {
-        cch = 0;
-        if (++cg == a.grp) { cg = 0; ++cx; }
-      }
-      if (++cstg == C::NSTAGE) cstg = 0;
-
-      // valid iff query row (within block i) >= tmin, and the key is in range
-      int tmin = -(1 << 30);
-      bool kok = true;
-      if (kind == KIND_DIAG) tmin = u;
-      else if (kind == KIND_PAD) kok = keyok;
-      else if (kind == KIND_ABS) {
-        const int64_t tm = (int64_t)u - (i - j) * BS;
-        tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);
-        kok = keyok;
-      }
-      tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
-
-      // the chunk's query rows in parts of HR (32) rows, one after the other:
-      // the per-part S, dP, P, dS and row statistics stay in few registers
-      // (unrolled at d <= 64: the parts' LDS addresses become instruction offsets)
-      constexpr int HUNROLL = D <= 64 ? 2 : 1;
-#pragma unroll HUNROLL
-      for (int h = 0; h < C::KC / HR; ++h) {
-        const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
-        const float2 *Mh = Ms + h * HR;
-        const int th = tmin - h * HR;
-        if constexpr (ROLES == 2) {
-          f32x4 xacc[HR / 16];
-          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
-          // element m of this lane at s_xch[(m * KEYS/16 + kw) * 64 + lane]: a wave's
-          // 16-byte accesses are consecutive, on distinct banks
-          float4 *xs = s_xch + kw * 64 + lane;
-          constexpr int XS = (KEYS / 16) * 64;  // stride between the parts m
-          float x[HR / 16][4];
-          if (role == 0) {
-#pragma unroll
-            for (int m = 0; m < HR / 16; ++m) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const float2 ms = Mh[16 * m + 4 * g + r];
-                const bool ok = kok && (16 * m + r >= th);
-                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, gt - ms.x));
-                asm volatile("" : "+v"(ev));
-                x[m][r] = ok ? ev : 0.f;
+        // the chunk's query rows in parts of HR (32) rows, one after the other:
+        // the per-part S, dP, P, dS and row statistics stay in few registers
+        // (unrolled at d <= 64: the parts' LDS addresses become instruction offsets)
+        constexpr int HUNROLL = D <= 64 ? 2 : 1;
+  #pragma unroll HUNROLL
+        for (int h = 0; h < C::KC / HR; ++h) {
+          const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
+          const float2 *Mh = Ms + h * HR;
+          const int th = tmin - h * HR;
+          if constexpr (ROLES == 2) {
+            f32x4 xacc[HR / 16];
+            mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(role ? Dh : Qh, kf, xacc, g, p);  // role 0: S, role 1: dP
+            // element m of this lane at s_xch[(m * KEYS/16 + kw) * 64 + lane]: a wave's
+            // 16-byte accesses are consecutive, on distinct banks
+            float4 *xs = s_xch + kw * 64 + lane;
+            constexpr int XS = (KEYS / 16) * 64;  // stride between the parts m
+            float x[HR / 16][4];
+            if (role == 0) {
+  #pragma unroll
+              for (int m = 0; m < HR / 16; ++m) {
+  #pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float2 ms = Mh[16 * m + 4 * g + r];
+                  const bool ok = kok && (16 * m + r >= th);
+                  float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                  asm volatile("" : "+v"(ev));
+                  x[m][r] = ok ? ev : 0.f;
+                }
+                xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
               }
-              xs[m * XS] = make_float4(x[m][0], x[m][1], x[m][2], x[m][3]);
             }
-          }
-          lds_barrier();  // P of this part is in LDS for the role-1 waves
-          if (role == 0) {
-            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Dh, x, dvacc, g, p);  // dV^T += dO^T P
-          } else {
-#pragma unroll
-            for (int m = 0; m < HR / 16; ++m) {
-              const float4 pv = xs[m * XS];
-              const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-              for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
+            lds_barrier();  // P of this part is in LDS for the role-1 waves
+            if (role == 0) {
+              tr_acc(SPC, Dh, x, dvacc);  // dV^T += dO^T P
+            } else {
+  #pragma unroll
+              for (int m = 0; m < HR / 16; ++m) {
+                const float4 pv = xs[m * XS];
+                const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+  #pragma unroll
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
+              }
+              tr_acc(SPC, Qh, x, dvacc);  // dK^T += Q^T dS
             }
-            mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Qh, x, dvacc, g, p);  // dK^T += Q^T dS
+            continue;
           }
-          continue;
-        }
-        f32x4 sacc[HR / 16], dpacc[HR / 16];
-        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
-        mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p);  // dP
-        float pp[HR / 16][4], ds[HR / 16][4];
-        // every exponential is computed unconditionally; masked elements of
-        // a masked chunk kind are then replaced by zeros in one uniform branch
-        // (unmasked chunks, the common case, skip the compares)
-#pragma unroll
-        for (int m = 0; m < HR / 16; ++m)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float2 ms = Mh[16 * m + 4 * g + r];
-            const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, gt - ms.x));
-            pp[m][r] = ev;
-            ds[m][r] = ev * (dpacc[m][r] - ms.y);
-          }
-        if (kind != KIND_FULL) {
-#pragma unroll
+          f32x4 sacc[HR / 16], dpacc[HR / 16];
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p);  // dP
+          float pp[HR / 16][4], ds[HR / 16][4];
+          // every exponential is computed unconditionally; masked elements of
+          // a masked chunk kind are then replaced by zeros in one uniform branch
+          // (unmasked chunks, the common case, skip the compares)
+  #pragma unroll
           for (int m = 0; m < HR / 16; ++m)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (!(kok && (16 * m + r >= th))) { pp[m][r] = 0.f; ds[m][r] = 0.f; }
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float2 ms = Mh[16 * m + 4 * g + r];
+              const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+              pp[m][r] = ev;
+              ds[m][r] = ev * (dpacc[m][r] - ms.y);
+            }
+          if (kind != KIND_FULL) {
+  #pragma unroll
+            for (int m = 0; m < HR / 16; ++m)
+  #pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (!(kok && (16 * m + r >= th))) { pp[m][r] = 0.f; ds[m][r] = 0.f; }
+          }
+          tr_acc(SPC, Dh, pp, dvacc);  // dV^T += dO^T P
+          tr_acc(SPC, Qh, ds, dkacc);  // dK^T += Q^T dS
         }
-        mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Dh, pp, dvacc, g, p);  // dV^T += dO^T P
-        mm_tr_acc<T, D, HR, (D >= 128 ? FBSA_BWD_TRWIN : 0)>(Qh, ds, dkacc, g, p);  // dK^T += Q^T dS
       }
     }
+  };
+  auto walk_g = [&](auto SPC) {
+    if (a.gate) walk(SPC, std::true_type{});
+    else walk(SPC, std::false_type{});
+  };
+  if constexpr (SPLIT) {
+    if (split) walk_g(std::true_type{});
+    else walk_g(std::false_type{});
+  } else {
+    walk_g(std::false_type{});
   }
 
   if (slot >= 0) {  // one segment of a split list: fp32 partials, summed by dkdv_reduce_kernel
@@ -1250,7 +1408,7 @@ static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, Bw
   } else {
     a.dout = dout;
   }
-  a.rowstat = (const float2 *)(ws + lay.rowstat);
+  a.rowstat = (float2 *)(ws + lay.rowstat);
   a.seg_off = (const int32_t *)(ws + lay.seg_off);
   a.ent = (const int32_t *)(ws + lay.vals_out);
   a.scale = d->scale;
@@ -1266,12 +1424,16 @@ template <typename K> static int set_lds(K kern, size_t lds, const char *what) {
   return lds_optin((const void *)kern, lds, "hipFuncSetAttribute(bwd)");
 }
 
-template <typename T, int BS, int D, bool DENSE> static int launch_dq_as(const BwdArgs &a, hipStream_t s) {
+template <typename T, int BS, int D, bool DENSE, bool DG> static int launch_dq_as(const BwdArgs &a, hipStream_t s) {
   using C = BwdCfg<T, BS, D, FBSA_DQ_LDS_BUDGET, 0>;
-  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES + (DENSE ? 0 : (size_t)a.kk * 16 + (size_t)C::NW * a.kk * 4);
-  int e = set_lds(dq_kernel<T, BS, D, DENSE>, lds, "fbsa_bwd_dq");
+  // slot tables (block, kind, gate: 12 bytes per slot; with the gate gradient
+  // also each entry's selection slot) and the gate gradient's per-wave and
+  // per-row scratch
+  const size_t lds = (size_t)C::NSTAGE * C::STAGE_BYTES +
+                     (DENSE ? 0 : (size_t)a.kk * (DG ? 16 : 12) + (DG ? (2 * C::NW + BS) * 4 : 0));
+  int e = set_lds(dq_kernel<T, BS, D, DENSE, DG>, lds, "fbsa_bwd_dq");
   if (e) return e;
-  hipLaunchKernelGGL((dq_kernel<T, BS, D, DENSE>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((dq_kernel<T, BS, D, DENSE, DG>), dim3((unsigned)(a.B * a.Hq * a.nblk)), dim3(C::NT), lds, s, a);
   return hip_check(hipGetLastError(), "dq_kernel launch");
 }
 
@@ -1292,7 +1454,8 @@ template <typename T, int BS, int D, bool DENSE> static int launch_dkdv_as(const
 // the dense (list-less) forms are their own instantiations (the list path's
 // code is unchanged by them)
 template <typename T, int BS, int D> static int launch_dq(const BwdArgs &a, hipStream_t s) {
-  return a.dense ? launch_dq_as<T, BS, D, true>(a, s) : launch_dq_as<T, BS, D, false>(a, s);
+  if (a.dense) return launch_dq_as<T, BS, D, true, false>(a, s);  // dense lists carry no gate
+  return a.dgate_part ? launch_dq_as<T, BS, D, false, true>(a, s) : launch_dq_as<T, BS, D, false, false>(a, s);
 }
 template <typename T, int BS, int D> static int launch_dkdv(const BwdArgs &a, hipStream_t s) {
   return a.dense ? launch_dkdv_as<T, BS, D, true>(a, s) : launch_dkdv_as<T, BS, D, false>(a, s);
@@ -1334,6 +1497,7 @@ int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, con
   fill_bwd(d, lay, ws, a, dout);
   a.q = q; a.k = k; a.v = v; a.sel = sel; a.gate = gate; a.dq = dq; a.dk = a.dv = nullptr;
   a.dgate_part = dgate ? (float *)(ws + lay.dgate_part) : nullptr;
+  a.pmass = (float *)(ws + lay.pmass);
   int e = bwd_dispatch(d, a, true, s);
   if (e || !dgate) return e;
   const int64_t n = d->B * d->hsel * d->nblk * d->kk;

@@ -268,6 +268,44 @@ template <typename T> __device__ __forceinline__ s16x8 pack8(const float *x) {
   return r;
 }
 
+// Two-term split of fp32 values into a 16-bit MFMA operand pair: hi = x
+// in T (rounded, or for bf16 truncated), lo = (x - hi) rounded to T (x - hi is
+// exact in fp32). A product with an exact 16-bit operand then takes two MFMAs
+// (hi, then lo into the same accumulator) and carries x to about 2^-16
+// relative for bf16 instead of the 2^-9 of one rounding.
+// bf16: hi is x truncated to its upper 16 bits (the pair gathered by one
+// v_perm_b32), lo = x - hi (exact) rounded once; three VALU ops per value.
+template <typename T> __device__ __forceinline__ void pack8_split(const float *x, s16x8 &hi, s16x8 &lo) {
+  float r[8];
+  if constexpr (__is_same(T, bf16)) {
+    u32x4 hw;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = __float_as_uint(x[2 * j]), b = __float_as_uint(x[2 * j + 1]);
+      hw[j] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // (b >> 16) << 16 | a >> 16
+      r[2 * j] = x[2 * j] - __uint_as_float(a & 0xFFFF0000u);
+      r[2 * j + 1] = x[2 * j + 1] - __uint_as_float(b & 0xFFFF0000u);
+    }
+    hi = __builtin_bit_cast(s16x8, hw);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const T h = (T)x[e];
+      hi[e] = bits16<T>(h);
+      r[e] = x[e] - (float)h;
+    }
+  }
+  lo = pack8<T>(r);
+}
+template <typename T> __device__ __forceinline__ void pack4_split(const float *x, s16x4 &hi, s16x4 &lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const T h = (T)x[e];
+    hi[e] = bits16<T>(h);
+    lo[e] = bits16<T>((T)(x[e] - (float)h));
+  }
+}
+
 // XCD-aware work order: launch order bid is dispatched round-robin over the
 // 8 XCDs; returning w = (bid % 8) * (n / 8) + bid / 8 gives each XCD a
 // contiguous range of the work order (the tail beyond 8*(n/8) maps 1:1).

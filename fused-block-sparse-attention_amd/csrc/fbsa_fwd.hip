@@ -221,14 +221,15 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   // than TAU (so p <= 2^TAU); each lane checks its own scores and only when
   // one does is the per-query chunk max formed across lanes.
   constexpr float TAU = 8.f;
+  // l_run: this lane's part of the row sum of P, summed in fp32 from the
+  // unrounded exponentials (the LSE the backward recomputes P from is then not
+  // perturbed by the rounding of P to the MFMA operand type)
   float m_run[QT], l_run[QT];
   f32x4 oacc[QT][D / 16];
-  f32x4 lacc[QT];  // 16-bit types: row sums of P from the PV MFMA (a tile of ones)
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     m_run[qt] = -INFINITY;
     l_run[qt] = 0.f;
-    lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mt = 0; mt < D / 16; ++mt) oacc[qt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -380,8 +381,6 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
           const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - mc);  // 0 when m_run = -inf
           l_run[qt] *= alpha;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) lacc[qt][r] *= alpha;
-#pragma unroll
           for (int mt = 0; mt < D / 16; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) oacc[qt][mt][r] *= alpha;
@@ -399,14 +398,16 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) sv[m][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qt][m][r], a.scale2, off));
 
-      // O^T += V^T P^T (and, for 16-bit types, the row sums of P as one more tile)
-      if constexpr (F32) {
+      // row sums of the unrounded P (this lane's keys), then O^T += V^T P^T
+      {
         float psum = 0.f;
 #pragma unroll
         for (int m = 0; m < C::KC / 16; ++m)
 #pragma unroll
           for (int r = 0; r < 4; ++r) psum += sv[m][r];
         l_run[qt] += psum;
+      }
+      if constexpr (F32) {
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt)
 #pragma unroll
@@ -418,8 +419,6 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
               oacc[qt][mt] = mfma_f32_16x16x4(vf, sv[m][r], oacc[qt][mt]);
             }
       } else if constexpr (C::KC >= 32) {
-        constexpr short ONE = (short)(__is_same(T, bf16) ? 0x3F80 : 0x3C00);
-        const s16x8 ones = {ONE, ONE, ONE, ONE, ONE, ONE, ONE, ONE};
         s16x8 pf[C::KC / 32];
 #pragma unroll
         for (int k2 = 0; k2 < C::KC / 32; ++k2) {
@@ -427,7 +426,6 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) { x[r] = sv[2 * k2][r]; x[4 + r] = sv[2 * k2 + 1][r]; }
           pf[k2] = pack8<T>(x);
-          lacc[qt] = Mfma16<T>::run(ones, pf[k2], lacc[qt]);
         }
         if (qt == 0) lds_wait_all();
 #pragma unroll
@@ -442,12 +440,9 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
           }
       } else {
         // KC == 16: one 16x16x16 MFMA per d tile
-        constexpr short ONE = (short)(__is_same(T, bf16) ? 0x3F80 : 0x3C00);
-        const s16x4 ones = {ONE, ONE, ONE, ONE};
         s16x4 pf;
 #pragma unroll
         for (int r = 0; r < 4; ++r) pf[r] = bits16<T>((T)sv[0][r]);
-        lacc[qt] = Mfma16<T>::run16(ones, pf, lacc[qt]);
         if (qt == 0) lds_wait_all();
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
@@ -461,13 +456,9 @@ __global__ __launch_bounds__(BS * 4 / QT) void fwd_kernel(FwdArgs a) {
   // ---- 4. epilogue ----
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    float lt;
-    if constexpr (F32) {
-      lt = l_run[qt] + shfl_xor_f(l_run[qt], 16);
-      lt += shfl_xor_f(lt, 32);
-    } else {
-      lt = lacc[qt][0];  // every row of the ones-tile holds the full sum for query p
-    }
+    // the query's four lanes (g = 0..3) hold its row sum in parts
+    float lt = l_run[qt] + shfl_xor_f(l_run[qt], 16);
+    lt += shfl_xor_f(lt, 32);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     T *orow = (T *)a.o + b * a.so[0] + hq * a.so[1] + (i * BS + tq[qt]) * a.so[2];
     const T *ogrow = a.og ? (const T *)a.og + b * a.sog[0] + hq * a.sog[1] + (i * BS + tq[qt]) * a.sog[2] : nullptr;

@@ -52,7 +52,7 @@ struct BwdLayout {
   int64_t n;       // sort entries: B * hsel * nblk * kk
   int64_t nseg;    // CSR segments: B * hsel * nblk
   int end_bit;     // radix-sort key bits
-  size_t rowstat, dout_attn, dgate_part, keys_in, keys_out, vals_in, vals_out, seg_off, sort_tmp;
+  size_t rowstat, dout_attn, dgate_part, pmass, keys_in, keys_out, vals_in, vals_out, seg_off, sort_tmp;
   size_t sort_tmp_bytes, total;
   // dK/dV list segments: a (b, KV head, key block) whose list is longer than
   // seg_entries (0: never) is walked by several workgroups that write fp32

@@ -97,49 +97,132 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
 
 // TW > 0 (16-bit types, KC >= 32): the transposed reads go out in a sliding
 // window of TW output tiles, each tile's MFMAs waiting only for its own reads.
-template <typename T, int D, int KC, int TW = 0>
-__device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC / 16][4], f32x4 *acc, int g, int p) {
+// SPLIT (16-bit types): x enters the product as a hi/lo operand pair
+// (pack8_split), two MFMAs per read, so the product carries x to ~2^-17
+// relative instead of one 16-bit rounding. NX = 2: a second operand x2
+// (plain 16-bit rounding) is accumulated into acc2 from the same tile reads.
+template <typename T, int D, int KC, int TW = 0, bool SPLIT = false, int NX = 1>
+__device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC / 16][4], f32x4 *acc, int g, int p,
+                                          const float (*x2)[4] = nullptr, f32x4 *acc2 = nullptr) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
-  if constexpr (sizeof(T) == 2 && KC >= 32 && TW > 0) {
-    s16x8 pk[KC / 32];
+  constexpr bool SP = SPLIT && sizeof(T) == 2;
+  if constexpr (sizeof(T) == 2 && KC >= 32) {
+    s16x8 pk[KC / 32], pkl[SP ? KC / 32 : 1], pk2[NX == 2 ? KC / 32 : 1];
 #pragma unroll
     for (int k2 = 0; k2 < KC / 32; ++k2) {
       float y[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) { y[r] = x[2 * k2][r]; y[4 + r] = x[2 * k2 + 1][r]; }
-      pk[k2] = pack8<T>(y);
-    }
-    constexpr int NTL = D / 16, RPT = 2 * (KC / 32);  // output tiles, reads per tile
-    constexpr int W = TW < NTL ? TW : NTL, VL = NTL < 8 ? NTL : 8;
-    s16x4 lo[NTL][KC / 32], hi[NTL][KC / 32];
-    // tile t, rows 32 k2 + 4g + p/4 (+16): lane base vb[t % 8] plus a constant
-    unsigned vb[VL];
+      if constexpr (SP) pack8_split<T>(y, pk[k2], pkl[k2]);
+      else pk[k2] = pack8<T>(y);
+      if constexpr (NX == 2) {
 #pragma unroll
-    for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
-    auto rd = [&](auto TT) {
-      constexpr int t = decltype(TT)::value;
-      static_for<KC / 32>([&](auto K2) {
-        constexpr int k2 = decltype(K2)::value, off = (t / 8) * 256 + k2 * 512 * CPR;
-        lo[t][k2] = lds_read_tr16_at<off>(vb[t % 8]);
-        hi[t][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[t % 8]);
-      });
-    };
-    static_for<W>(rd);
-    static_for<NTL>([&](auto TT) {
-      constexpr int t = decltype(TT)::value;
-      constexpr int last = t + W - 1 < NTL - 1 ? t + W - 1 : NTL - 1;  // last tile requested so far
-      constexpr int n = (last - t) * RPT;
-      lds_wait_le<(n < 15 ? n : 15)>();
+        for (int r = 0; r < 4; ++r) { y[r] = x2[2 * k2][r]; y[4 + r] = x2[2 * k2 + 1][r]; }
+        pk2[k2] = pack8<T>(y);
+      }
+    }
+    // an output tile's A operands from its transposed reads; its hi products
+    // (and the second operand's); its lo products, issued one tile later so
+    // that they do not wait on the hi products of the same accumulator
+    auto tile_av = [&](s16x8 (&av)[KC / 32], s16x4 (&lo)[KC / 32], s16x4 (&hi)[KC / 32]) {
 #pragma unroll
       for (int k2 = 0; k2 < KC / 32; ++k2) {
-        lds_ready(lo[t][k2]);
-        lds_ready(hi[t][k2]);
-        const s16x4 a = lo[t][k2], b = hi[t][k2];
-        const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        acc[t] = Mfma16<T>::run(av, pk[k2], acc[t]);
+        lds_ready(lo[k2]);
+        lds_ready(hi[k2]);
+        const s16x4 a = lo[k2], b = hi[k2];
+        av[k2] = s16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
       }
-      if constexpr (t + W < NTL) rd(std::integral_constant<int, t + W>{});
-    });
+    };
+    auto tile_hi = [&](const s16x8 (&av)[KC / 32], f32x4 &at, f32x4 &a2t) {
+#pragma unroll
+      for (int k2 = 0; k2 < KC / 32; ++k2) at = Mfma16<T>::run(av[k2], pk[k2], at);
+      if constexpr (NX == 2) {
+#pragma unroll
+        for (int k2 = 0; k2 < KC / 32; ++k2) a2t = Mfma16<T>::run(av[k2], pk2[k2], a2t);
+      }
+    };
+    auto tile_lo = [&](const s16x8 (&av)[KC / 32], f32x4 &at) {
+      if constexpr (SP) {
+#pragma unroll
+        for (int k2 = 0; k2 < KC / 32; ++k2) at = Mfma16<T>::run(av[k2], pkl[k2], at);
+      }
+    };
+    constexpr int NTL = D / 16;
+    if constexpr (TW > 0) {
+      constexpr int RPT = 2 * (KC / 32);  // reads per tile
+      constexpr int W = TW < NTL ? TW : NTL, VL = NTL < 8 ? NTL : 8;
+      s16x4 lo[NTL][KC / 32], hi[NTL][KC / 32];
+      s16x8 avp[KC / 32];  // the previous tile's operands (its lo products are pending)
+      // tile t, rows 32 k2 + 4g + p/4 (+16): lane base vb[t % 8] plus a constant
+      unsigned vb[VL];
+#pragma unroll
+      for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
+      auto rd = [&](auto TT) {
+        constexpr int t = decltype(TT)::value;
+        static_for<KC / 32>([&](auto K2) {
+          constexpr int k2 = decltype(K2)::value, off = (t / 8) * 256 + k2 * 512 * CPR;
+          lo[t][k2] = lds_read_tr16_at<off>(vb[t % 8]);
+          hi[t][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[t % 8]);
+        });
+      };
+      static_for<W>(rd);
+      static_for<NTL>([&](auto TT) {
+        constexpr int t = decltype(TT)::value;
+        constexpr int last = t + W - 1 < NTL - 1 ? t + W - 1 : NTL - 1;  // last tile requested so far
+        constexpr int n = (last - t) * RPT;
+        lds_wait_le<(n < 15 ? n : 15)>();
+        s16x8 av[KC / 32];
+        tile_av(av, lo[t], hi[t]);
+        tile_hi(av, acc[t], NX == 2 ? acc2[t] : acc[t]);
+        if constexpr (t > 0) tile_lo(avp, acc[t - 1]);
+        if constexpr (SP) {
+#pragma unroll
+          for (int k2 = 0; k2 < KC / 32; ++k2) avp[k2] = av[k2];
+        }
+        if constexpr (t + W < NTL) rd(std::integral_constant<int, t + W>{});
+      });
+      tile_lo(avp, acc[NTL - 1]);
+    } else {
+      // the transposed reads go out in batches of up to 8 output tiles (all of
+      // them for d <= 128), each batch waited for once, so d = 256 does not hold
+      // every tile's operands in registers at the same time
+      constexpr int TB = NTL < 8 ? NTL : 8, VL = TB;
+      unsigned vb[VL];
+#pragma unroll
+      for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
+#pragma unroll
+      for (int t0 = 0; t0 < NTL; t0 += TB) {
+        s16x4 lo[TB][KC / 32], hi[TB][KC / 32];
+        static_for<TB>([&](auto TT) {
+          constexpr int tt = decltype(TT)::value;
+          static_for<KC / 32>([&](auto K2) {
+            constexpr int k2 = decltype(K2)::value, off = k2 * 512 * CPR;
+            // tile t0 + tt: lane base vb[tt] (t0 is a multiple of 8) plus (t0 / 8) * 256
+            lo[tt][k2] = lds_read_tr16_at<off>(vb[tt] + (t0 / 8) * 256);
+            hi[tt][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[tt] + (t0 / 8) * 256);
+          });
+        });
+        lds_wait_all();
+        if constexpr (SP) {
+          // every tile's hi products, then every tile's lo products
+          s16x8 av[TB][KC / 32];
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            tile_av(av[tt], lo[tt], hi[tt]);
+            tile_hi(av[tt], acc[t0 + tt], NX == 2 ? acc2[t0 + tt] : acc[t0 + tt]);
+          }
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) tile_lo(av[tt], acc[t0 + tt]);
+        } else {
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            s16x8 av[KC / 32];
+            tile_av(av, lo[tt], hi[tt]);
+            tile_hi(av, acc[t0 + tt], NX == 2 ? acc2[t0 + tt] : acc[t0 + tt]);
+          }
+        }
+      }
+    }
     return;
   }
   if constexpr (sizeof(T) == 4) {
@@ -152,55 +235,24 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
           const int row = 16 * m + 4 * g + r;
           const float a = *(const float *)(tile + (row * CPR + ((4 * t + (p >> 2)) ^ swz(row, CPR))) * 16 + (p & 3) * 4);
           acc[t] = mfma_f32_16x16x4(a, x[m][r], acc[t]);
+          if constexpr (NX == 2) acc2[t] = mfma_f32_16x16x4(a, x2[m][r], acc2[t]);
         }
       // keeps the next tile's loads from being hoisted above these MFMAs (at
       // d >= 128 the hoisted loads of every tile exhaust the registers)
       if constexpr (D >= 128) asm volatile("" ::: "memory");
     }
-  } else if constexpr (KC >= 32) {
-    s16x8 pk[KC / 32];
-#pragma unroll
-    for (int k2 = 0; k2 < KC / 32; ++k2) {
-      float y[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) { y[r] = x[2 * k2][r]; y[4 + r] = x[2 * k2 + 1][r]; }
-      pk[k2] = pack8<T>(y);
-    }
-    // the transposed reads go out in batches of up to 8 output tiles (all of
-    // them for d <= 128), each batch waited for once, so d = 256 does not hold
-    // every tile's operands in registers at the same time
-    constexpr int TB = D / 16 < 8 ? D / 16 : 8, VL = TB;
-    unsigned vb[VL];
-#pragma unroll
-    for (int l = 0; l < VL; ++l) vb[l] = (unsigned)(uintptr_t)tile + tile_vbase(l, g, p, CPR);
-#pragma unroll
-    for (int t0 = 0; t0 < D / 16; t0 += TB) {
-      s16x4 lo[TB][KC / 32], hi[TB][KC / 32];
-      static_for<TB>([&](auto TT) {
-        constexpr int tt = decltype(TT)::value;
-        static_for<KC / 32>([&](auto K2) {
-          constexpr int k2 = decltype(K2)::value, off = k2 * 512 * CPR;
-          // tile t0 + tt: lane base vb[tt] (t0 is a multiple of 8) plus (t0 / 8) * 256
-          lo[tt][k2] = lds_read_tr16_at<off>(vb[tt] + (t0 / 8) * 256);
-          hi[tt][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[tt] + (t0 / 8) * 256);
-        });
-      });
-      lds_wait_all();
-#pragma unroll
-      for (int tt = 0; tt < TB; ++tt)
-#pragma unroll
-        for (int k2 = 0; k2 < KC / 32; ++k2) {
-          lds_ready(lo[tt][k2]);
-          lds_ready(hi[tt][k2]);
-          const s16x4 a = lo[tt][k2], b = hi[tt][k2];
-          const s16x8 av = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-          acc[t0 + tt] = Mfma16<T>::run(av, pk[k2], acc[t0 + tt]);
-        }
-    }
   } else {
-    s16x4 pk;
+    // KC == 16: one 16x16x16 MFMA per d tile (and per split part / operand)
+    s16x4 pk, pkl, pk2;
+    if constexpr (SP) pack4_split<T>(x[0], pk, pkl);
+    else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)x[0][r]);
+      for (int r = 0; r < 4; ++r) pk[r] = bits16<T>((T)x[0][r]);
+    }
+    if constexpr (NX == 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pk2[r] = bits16<T>((T)x2[0][r]);
+    }
     s16x4 a[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
@@ -213,6 +265,11 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
     for (int t = 0; t < D / 16; ++t) {
       lds_ready(a[t]);
       acc[t] = Mfma16<T>::run16(a[t], pk, acc[t]);
+      if constexpr (NX == 2) acc2[t] = Mfma16<T>::run16(a[t], pk2, acc2[t]);
+    }
+    if constexpr (SP) {
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) acc[t] = Mfma16<T>::run16(a[t], pkl, acc[t]);
     }
   }
 }

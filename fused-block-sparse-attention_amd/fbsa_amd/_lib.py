@@ -18,7 +18,7 @@ SCORE_DOT, SCORE_MAX2, SCORE_QUEST = 0, 1, 2
 SEL_OWN_FIRST, SEL_SORTED_SINK, SEL_SORTED_TOPK = 0, 1, 2
 QMAX_EXACT = 1
 SEL_CHUNK_SHIFT = 8
-FLAG_OUT_GATE, FLAG_DENSE = 1, 2
+FLAG_OUT_GATE, FLAG_DENSE, FLAG_DGATE = 1, 2, 4
 SELECT_SCRATCH_BYTES = 32 << 20   # FBSA_SELECT_SCRATCH_BYTES
 
 _i64x3 = ctypes.c_int64 * 3
@@ -103,21 +103,33 @@ SIGNATURES = {
 _lib = None
 
 
-def load():
-    """Load libfbsa.so once; raise if it is absent (no CPU fallback)."""
-    global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(LIB_PATH):
-        raise RuntimeError(f"fbsa: HIP library not built ({LIB_PATH} missing); "
+def open_library(path):
+    """ctypes handle of a libfbsa build at `path` with every entry point typed."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"fbsa: HIP library not built ({path} missing); "
                            "run `make -C fused-block-sparse-attention_amd`")
-    lib = ctypes.CDLL(LIB_PATH)
+    lib = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = lib
     return lib
+
+
+def load():
+    """Load libfbsa.so once; raise if it is absent (no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        _lib = open_library(LIB_PATH)
+    return _lib
+
+
+def use(lib):
+    """Route every op through `lib` (a handle from open_library; None restores
+    the default build on the next call). Returns the handle in use before."""
+    global _lib
+    prev, _lib = _lib, lib
+    return prev
 
 
 class FbsaError(RuntimeError):

@@ -218,7 +218,7 @@ def attention_backward(q, k, v, sel, o, lse, dout, *, mask, scale=None, gate=Non
     dog = torch.empty(B, Hq, L, Dp, dtype=q.dtype, device=dev) if og is not None else None
     d = make_desc(qk[0], qk[1], qk[2], o_p, sel32, mask=mask, scale=scale, l_valid=l_valid, dout=do_p,
                   out_gate=og)
-    d.flags |= _lib.FLAG_OUT_GATE if og is not None else 0
+    d.flags |= (_lib.FLAG_OUT_GATE if og is not None else 0) | (_lib.FLAG_DGATE if need_dgate else 0)
     lib = _lib.load()
     nbytes = lib.fbsa_bwd_workspace_bytes(d)
     if nbytes == 0:

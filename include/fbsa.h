@@ -68,7 +68,9 @@ int fbsa_version(void);
 
 /* Fused block-sparse forward. o = softmax(scale*q.k^T + gate) v over the
  * selected key blocks (times sigmoid(out_gate) when out_gate != NULL);
- * lse (nullable) = natural-log normaliser of the un-gated softmax.
+ * lse (nullable) = natural-log normaliser of the un-gated softmax, summed in
+ * fp32 from the unrounded exponentials for every input dtype (16-bit P enters
+ * only the P.V product).
  * gate (nullable): fp32 additive bias per (b, hsel, i, slot).
  * Replaces _bsattn_fwd / bsattn_forward (src/triton_kernel.py:20-74, 184-207)
  * and the gather+SDPA of _gather_and_attend (src/ssa_model.py:57-90) and
@@ -251,8 +253,12 @@ int fbsa_select_qmax(const fbsa_qmax_desc *d, const void *a, const void *b1, con
  * length, and the backward's transposed lists need no sort (their total,
  * B * hsel * the number of (query block, key block) pairs, must stay below
  * 2^31). Replaces the SDPA fast path of blocksparse_forward
- * (src/qwen_blocksparse.py:37-41). */
-enum { FBSA_FLAG_OUT_GATE = 1, FBSA_FLAG_DENSE = 2 };
+ * (src/qwen_blocksparse.py:37-41).
+ * DGATE (backward): the gate gradient will be asked for (dgate != NULL); the
+ * workspace then also holds each query row's probability mass per slot
+ * (B*Hq*L*kk fp32), with which a 16-bit gate gradient is corrected to the
+ * row's fp32 delta. Required with dgate for 16-bit types. */
+enum { FBSA_FLAG_OUT_GATE = 1, FBSA_FLAG_DENSE = 2, FBSA_FLAG_DGATE = 4 };
 
 /* Workspace for the backward stages below (one opaque region, 256-byte
  * aligned): per-row softmax statistics, the block-transposed index (CSR of
@@ -278,14 +284,19 @@ int fbsa_transpose_index(const fbsa_attn_desc *d, const int32_t *sel, void *work
 /* Stage 3. dq (B,Hq,L,D contiguous) over each query block's selected key
  * blocks; when dgate != NULL also the fp32 gate gradient (B,Hsel,nblk,kk),
  * summed over the heads sharing a selection in a fixed order (0 for masked
- * slots). Needs stage 1. */
+ * slots). Needs stage 1. For 16-bit types it also replaces each row's delta in
+ * the workspace by sum P*dP over the row's keys, accumulated in fp32 from the
+ * unrounded P (the reference's D, src/triton_kernel.py:132-150); the gate
+ * gradient uses that delta. */
 int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
                 const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate,
                 void *workspace, size_t workspace_bytes, void *stream);
 
 /* Stage 4. dk, dv (B,Hkv,L,D contiguous), one workgroup per key block walking
  * its transposed list (and the GQA group's query heads) in order: no atomics,
- * bitwise repeatable. Needs stages 1 and 2. */
+ * bitwise repeatable. Needs stages 1 and 2, and stage 3 for the fp32-exact
+ * delta of 16-bit types (without it the prep's estimate from the stored O is
+ * used). */
 int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const void *v,
                   const void *dout, const float *gate, void *dk, void *dv, void *workspace,
                   size_t workspace_bytes, void *stream);

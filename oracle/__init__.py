@@ -15,9 +15,12 @@ select   : pooling (mean / min / max), pooled scores, selection conventions
            B (``_finish``, ``src/qwen_blocksparse.py:87-99``), near-tie census.
 attn     : gather attention forward/backward in float64 with the reference's
            three masking rules, plus dense closed forms.
+triton_arith : the reference Triton backward's own rounding points (TF32
+           dots, fp32 D, bf16 atomic sums; ``src/triton_kernel.py:77-181``),
+           to print its error beside the build's.
 
 Every function cites the reference file:line it restates. What pins each
 function (golden vectors, closed forms, brute force) is listed in
 ``tests/test_oracle_*.py``.
 """
-from . import numerics, select, attn  # noqa: F401
+from . import numerics, select, attn, triton_arith  # noqa: F401

@@ -66,9 +66,12 @@ def _census(name, score_oracle, picks_oracle, picks_ref, valid, k_row, score_ref
     differ = (a != b).any(-1)
     # the parity procedure on the oracle's scores, chosen set = the oracle's
     tie = osel.near_tie_rows(score_oracle, _set_rows(a), int(k_row.max()), valid)
-    # torch's fp32 accumulation can round a score one bf16 ulp away from the
-    # correctly rounded value the oracle holds; a row can then tie in torch's
-    # own scores where the oracle's are one ulp apart
+    # Rows outside north_star's near-tie rule: torch's fp32 accumulation can
+    # round a score one bf16 ulp away from the correctly rounded value the
+    # oracle (and the kernels) hold, so a row can tie in torch's own scores
+    # where the oracle's are one ulp apart. Such rows are not near ties under
+    # the rule; they are counted and reported as outside it, and each is
+    # checked to be exactly that one-ulp case
     sdiff = (score_oracle != score_ref) & valid
     tie_t = osel.near_tie_rows(score_ref, _set_rows(b), int(k_row.max()), valid)
     by_rounding = differ & ~tie & tie_t & sdiff.any(-1)
@@ -84,7 +87,7 @@ def _census(name, score_oracle, picks_oracle, picks_ref, valid, k_row, score_ref
         "differing_rows": int(differ.sum()), "near_tie_rows": int(tie.sum()),
         "differing_and_near_tie": int((differ & tie).sum()),
         "differing_exact_tie_at_k": int((differ & exact_tie).sum()),
-        "differing_by_torch_accumulation_rounding": int(by_rounding.sum()),
+        "differing_outside_near_tie_rule": int(by_rounding.sum()),
         "rows_where_torch_score_differs": int(sdiff.any(-1).sum()),
         "score_entries_differing": int(sdiff.sum()),
     }
@@ -145,7 +148,7 @@ def test_census_config3_mean_pooled():
     q = (torch.randn(*shape, generator=g) * 0.125).to(torch.bfloat16)
     k = (torch.randn(*shape, generator=g) * 0.125).to(torch.bfloat16)
     c = _run_conv_a("config 3", q, k, 64, 16)
-    assert c["differing_rows"] == c["differing_and_near_tie"] + c["differing_by_torch_accumulation_rounding"]
+    assert c["differing_rows"] == c["differing_and_near_tie"] + c["differing_outside_near_tie_rule"]
 
 
 @pytest.mark.slow
@@ -157,7 +160,7 @@ def test_census_config5_prefix_mean_pooled():
     q = torch.randn(*shape, generator=g).to(torch.bfloat16)
     k = torch.randn(*shape, generator=g).to(torch.bfloat16)
     c = _run_conv_a("config 5 prefix", q, k, 64, 16)
-    assert c["differing_rows"] == c["differing_and_near_tie"] + c["differing_by_torch_accumulation_rounding"]
+    assert c["differing_rows"] == c["differing_and_near_tie"] + c["differing_outside_near_tie_rule"]
 
 
 @pytest.mark.slow
@@ -199,4 +202,4 @@ def test_census_config4_select_max():
             total[key] = total.get(key, 0) + val
     _say("config 4 SelectMax total", total)
     assert total["differing_rows"] == (total["differing_and_near_tie"]
-                                       + total["differing_by_torch_accumulation_rounding"])
+                                       + total["differing_outside_near_tie_rule"])

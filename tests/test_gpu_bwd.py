@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import attn as oattn, select as osel
-from _util import randn, np64, assert_close, rel_l2, TOL, OUT_ROUND
+from _util import randn, np64, assert_close, TOL
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -37,6 +37,13 @@ def _cmp(got, ref, dtype, names=("dq", "dk", "dv")):
         print(f"  {n}: max_abs={ma:.2e} rel_l2={rl:.2e}", flush=True)
 
 
+def _cmp_mag(got, ref, dtype, names=("dq", "dk", "dv")):
+    # the absolute bar, printing each output's largest magnitude beside its error
+    for n, gv, rv in zip(names, got, ref):
+        ma, rl = assert_close(gv, rv, dtype, n)
+        print(f"  {n}: max|ref|={float(np.max(np.abs(rv))):.1f} max_abs={ma:.2e} rel_l2={rl:.2e}", flush=True)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_config1_shape(dtype):
     g = torch.Generator().manual_seed(0)
@@ -57,14 +64,15 @@ def test_config2_gate_bias_and_dgate():
     got = _gpu_bwd(q, k, v, sel[:, None], do, "slot_causal", gate=gate, need_dgate=True)
     ref = _oracle(q, k, v, sel[:, None], do, "slot_causal", gate=gate)
     _cmp(got[:3], ref[:3], "bf16")
-    # dgate (fp32) sums bs*bs*H score gradients per slot: relative-L2 1e-2, and
-    # max-abs 2e-2 relative to the largest magnitude
+    # dgate (fp32 output) sums bs*bs*H = 8192 score gradients per slot, each
+    # formed with the row's delta as sum P dP (the prep's 16-bit-O estimate
+    # corrected by its error times the slot's probability mass): the absolute
+    # bf16 bar
     dg, rdg = got[3], ref[3]
     rl = float(np.linalg.norm(dg - rdg) / np.linalg.norm(rdg))
-    ma = float(np.max(np.abs(dg - rdg)) / max(1.0, np.max(np.abs(rdg))))
-    print(f"  dgate: max_abs={float(np.max(np.abs(dg - rdg))):.2e} max|ref|={float(np.max(np.abs(rdg))):.1f} "
-          f"max_abs/max|ref|={ma:.2e} rel_l2={rl:.2e}", flush=True)
-    assert rl <= 1e-2 and ma <= 2e-2
+    ma = float(np.max(np.abs(dg - rdg)))
+    print(f"  dgate: max_abs={ma:.2e} max|ref|={float(np.max(np.abs(rdg))):.1f} rel_l2={rl:.2e}", flush=True)
+    assert ma <= TOL["bf16"]["max_abs"] and rl <= TOL["bf16"]["rel_l2"]
 
 
 def test_config2_output_gate():
@@ -128,18 +136,9 @@ def test_long_lists_walked_in_segments(dtype):
     got = _gpu_bwd(q, k, v, sel, do, "none")
     ref = _oracle(q, k, v, sel, do, "none")
     # a split list sums at least 4096 * 16 query rows per key, so block 0's dK/dV
-    # is large; in 16-bit dtypes it carries the rounding of dS to the input dtype
-    # (before its product, as in the reference kernel) in proportion: max-abs
-    # relative to the largest magnitude (as for dgate), relative L2 unscaled.
-    # fp32 keeps the absolute 1e-4 bar.
-    t = TOL[dtype]
-    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
-        mag = max(1.0, float(np.max(np.abs(rv))))
-        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND[dtype] * np.abs(rv)))
-        rl = rel_l2(gv, rv)
-        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
-        bound = t["max_abs"] * (1.0 if dtype == "f32" else mag)
-        assert excess <= bound and rl <= t["rel_l2"], n
+    # is large (|dK| ~ 40); 16-bit P and dS enter its products as hi/lo pairs,
+    # so the absolute bar of the dtype holds (beyond the output's own rounding)
+    _cmp_mag(got[:3], ref[:3], dtype)
 
 
 def test_duplicate_heavy_list_segments_half_blocks():
@@ -156,13 +155,7 @@ def test_duplicate_heavy_list_segments_half_blocks():
     sel[..., 0] = np.arange(nblk)
     got = _gpu_bwd(q, k, v, sel, do, "none")
     ref = _oracle(q, k, v, sel, do, "none")
-    t = TOL["bf16"]
-    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
-        mag = max(1.0, float(np.max(np.abs(rv))))  # block 0 sums 166 * 8 * 128 rows (see above)
-        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND["bf16"] * np.abs(rv)))
-        rl = rel_l2(gv, rv)
-        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
-        assert excess <= t["max_abs"] * mag and rl <= t["rel_l2"], n
+    _cmp_mag(got[:3], ref[:3], "bf16")  # block 0 sums 166 * 8 * 128 rows (see above)
 
 
 @pytest.mark.parametrize("dtype,D", [("bf16", 64), ("f32", 32)])
@@ -180,14 +173,7 @@ def test_segments_of_small_blocks(dtype, D):
     sel[..., 0] = np.arange(nblk)
     got = _gpu_bwd(q, k, v, sel, do, "none")
     ref = _oracle(q, k, v, sel, do, "none")
-    t = TOL[dtype]
-    for n, gv, rv in zip(("dq", "dk", "dv"), got[:3], ref[:3]):
-        mag = max(1.0, float(np.max(np.abs(rv))))  # block 0 sums 1025 * 16 rows per head
-        excess = float(np.max(np.abs(gv - rv) - OUT_ROUND[dtype] * np.abs(rv)))
-        rl = rel_l2(gv, rv)
-        print(f"  {n}: max|ref|={mag:.1f} max_abs={excess:.2e} rel_l2={rl:.2e}", flush=True)
-        bound = t["max_abs"] * (1.0 if dtype == "f32" else mag)
-        assert excess <= bound and rl <= t["rel_l2"], n
+    _cmp_mag(got[:3], ref[:3], dtype)  # block 0 sums 1025 * 16 rows per head
 
 
 def test_backward_is_bitwise_repeatable():

@@ -112,3 +112,39 @@ def test_dense_long_sequence_forward_backward():
     rp = oattn.dense(np64(q[:, :, :P]), np64(k[:, :, :P]), np64(v[:, :, :P]), True)
     ro_np = rp[0] if isinstance(rp, tuple) else rp
     assert_close(np64(o[:, :, :P]), ro_np, "bf16", "o prefix vs oracle")
+
+
+def test_dense_fp32_long_lists_walked_in_segments():
+    # fp32, MASK_NONE, 2048 blocks of 16: every key block's implicit list holds
+    # all 2048 query blocks (x 2 query heads), so its fp32 dK/dV sums 65,536
+    # query rows; the dense lists are walked in segments like explicit ones
+    # (closed-form offsets), and the result meets the absolute fp32 bar against
+    # fp32 attention in torch (autograd)
+    from fbsa_amd import ops
+    B, Hq, Hkv, D, bs, nblk = 1, 2, 1, 32, 16, 2048
+    N = nblk * bs
+    g = torch.Generator(device=DEV).manual_seed(23)
+    rn = lambda *s: torch.randn(*s, generator=g, device=DEV)  # noqa: E731
+    q, k, v, do = rn(B, Hq, N, D), rn(B, Hkv, N, D), rn(B, Hkv, N, D), rn(B, Hq, N, D)
+    dense = ops.DenseSelection(B, nblk)
+    o, lse = ops.attention_forward(q, k, v, dense, mask=ops.MASK_NONE, need_lse=True)
+    dq, dk, dv = ops.attention_backward(q, k, v, dense, o, lse, do, mask=ops.MASK_NONE)[:3]
+    # torch fp32 reference: full (non-causal) attention, query chunks, GQA by repeat
+    kf = k.repeat_interleave(2, 1).detach().requires_grad_(True)
+    vf = v.repeat_interleave(2, 1).detach().requires_grad_(True)
+    ro = torch.empty_like(q)
+    rdq = torch.empty_like(q)
+    for r0 in range(0, N, 4096):
+        qc = q[:, :, r0:r0 + 4096].detach().requires_grad_(True)
+        oc = torch.matmul(torch.softmax(torch.matmul(qc, kf.transpose(-1, -2).contiguous()) * D ** -0.5, -1), vf)
+        ro[:, :, r0:r0 + 4096] = oc.detach()
+        (oc * do[:, :, r0:r0 + 4096]).sum().backward()
+        rdq[:, :, r0:r0 + 4096] = qc.grad
+    rdk = kf.grad.view(B, Hkv, 2, N, D).sum(2)
+    rdv = vf.grad.view(B, Hkv, 2, N, D).sum(2)
+    torch.cuda.synchronize()
+    for name, got, ref in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        err = float((got.double() - ref.double()).abs().max())
+        rl = float((got.double() - ref.double()).norm() / ref.double().norm())
+        _say(f"fp32 dense segments {name}: max_abs={err:.3e} rel_l2={rl:.3e} max|ref|={float(ref.abs().max()):.3g}")
+        assert err <= TOL["f32"]["max_abs"] and rl <= TOL["f32"]["rel_l2"], name

@@ -44,10 +44,10 @@ def _check(name, got, ref, dtype, tol_scale=1.0):
     return excess, rl
 
 
-# The forward's row sums add P after its rounding to the input dtype (the same
-# P that multiplies V), so a 16-bit LSE may differ from the exact one by up to
-# 2^-9 (relative error of the sum) in natural-log units.
-LSE_TOL = {"bf16": 2.0 ** -9 + 1e-5, "f16": 2.0 ** -12 + 1e-5, "f32": 1e-5}
+# The forward sums its row normalisers in fp32 from the unrounded exponentials
+# (the 16-bit rounding of P enters only the P.V product), so the LSE is an fp32
+# quantity for every input dtype.
+LSE_TOL = {"bf16": 1e-4, "f16": 1e-4, "f32": 1e-4}
 
 
 def _blocks(x, blocks, bs):
@@ -55,23 +55,44 @@ def _blocks(x, blocks, bs):
 
 
 # ---------------------------------------------------------------- configuration 3
-def test_config3_forward_all_rows():
+@pytest.fixture(scope="module")
+def cfg3():
+    # B1 H8 N262144 D64 bs64, top-16 own-first, slot-causal; q,k,v ~ N(0,1)/8, dO ~ N(0,1)
     from fbsa_amd import ops, selection
     g = torch.Generator().manual_seed(0)
     B, H, N, D, bs, topk = 1, 8, 262144, 64, 64, 16
     q, k, v = (randn(g, (B, H, N, D), "bf16", scale=0.125) for _ in range(3))
-    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    do = randn(g, (B, H, N, D), "bf16")
+    qd, kd, vd, dod = q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV)
     sel = selection.select_mean_pooled(qd, kd, bs, topk, True)[:, None]
     o, lse = ops.attention_forward(qd, kd, vd, sel, mask=ops.MASK_SLOT_CAUSAL, need_lse=True)
-    ro, rlse = _torchref.attention(qd, kd, vd, sel, "slot_causal", chunk=256)
+    grads = ops.attention_backward(qd, kd, vd, sel, o, lse, dod, mask=ops.MASK_SLOT_CAUSAL)
+    ref = _torchref.attention(qd, kd, vd, sel, "slot_causal", do=dod, chunk=256)
     torch.cuda.synchronize()
-    _check("config 3 o (all rows, fp32 torch)", o, ro, "bf16")
-    lerr = float((lse - rlse).abs().max())
+    return dict(q=q, k=k, v=v, do=do, sel=sel, o=o, lse=lse, grads=grads, ref=ref, bs=bs)
+
+
+def test_config3_forward_all_rows(cfg3):
+    c = cfg3
+    _check("config 3 o (all rows, fp32 torch)", c["o"], c["ref"][0], "bf16")
+    lerr = float((c["lse"] - c["ref"][1]).abs().max())
     _say(f"config 3 lse: max_abs={lerr:.3e}")
     assert lerr <= LSE_TOL["bf16"]
-    rows = [0, 1, 16, 17, 1000, 2048, 4095]
-    so, _ = oattn.fwd(np64(q), np64(k), np64(v), sel.cpu().numpy(), "slot_causal", rows=rows)
-    _check("config 3 o (sampled blocks, oracle)", _blocks(o, rows, bs).cpu(), so, "bf16")
+    rows, bs = [0, 1, 16, 17, 1000, 2048, 4095], c["bs"]
+    so, _ = oattn.fwd(np64(c["q"]), np64(c["k"]), np64(c["v"]), c["sel"].cpu().numpy(), "slot_causal", rows=rows)
+    _check("config 3 o (sampled blocks, oracle)", _blocks(c["o"], rows, bs).cpu(), so, "bf16")
+
+
+def test_config3_backward_all_rows(cfg3):
+    # dq on every query row, dk / dv on every key block, against the fp32 torch
+    # gather path's autograd (src/verify_kernel.py:15-39 compares the same three
+    # gradients against the gather path)
+    c = cfg3
+    dq, dk, dv = c["grads"][:3]
+    _, _, rdq, rdk, rdv, _ = c["ref"]
+    _check("config 3 dq (all rows, fp32 torch)", dq, rdq, "bf16")
+    _check("config 3 dk (all blocks, fp32 torch)", dk, rdk, "bf16")
+    _check("config 3 dv (all blocks, fp32 torch)", dv, rdv, "bf16")
 
 
 # ---------------------------------------------------------------- configuration 4
@@ -182,3 +203,43 @@ def test_gqa_token_causal_sink_segments(dtype):
            _blocks(torch.as_tensor(r[1]), [nblk - 1], bs), dtype)
     _check(f"sink segments {dtype} dv last block (oracle)", _blocks(dv[:, 1:], [nblk - 1], bs).cpu(),
            _blocks(torch.as_tensor(r[2]), [nblk - 1], bs), dtype)
+
+
+# ---------------------------------------------------------------- configuration 5
+def test_config5_forward_sampled_blocks():
+    # B1 H8 D64 N4194304 bs64 (nblk 65536), top-16 own-first, slot-causal: the
+    # selection-scaling stress shape. O of the first and last 8 query blocks and
+    # 40 random ones against the float64 oracle. Each sampled row is checked on
+    # a small problem made of its own block and the blocks it selects,
+    # renumbered in ascending order (the slot-causal rule only compares block
+    # indices, so an order-preserving renumbering keeps every mask decision).
+    from fbsa_amd import ops, selection
+    B, H, N, D, bs, topk = 1, 8, 4194304, 64, 64, 16
+    nblk = N // bs
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v = ((torch.randn(B, H, N, D, generator=g, device=DEV) * D ** -0.5).to(torch.bfloat16) for _ in range(3))
+    sel = selection.select_mean_pooled(q, k, bs, topk, True)[:, None]
+    o = ops.attention_forward(q, k, v, sel, mask=ops.MASK_SLOT_CAUSAL)
+    torch.cuda.synchronize()
+    _say("config 5 forward done")
+    sel_np = sel.cpu().numpy()
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(nblk - 8, nblk),
+                                     np.random.default_rng(5).integers(8, nblk - 8, 40)]))
+    worst = 0.0
+    for i in rows.tolist():
+        srow = sel_np[0, 0, i]
+        blocks = np.unique(np.concatenate([srow, [i]]))
+        rank = {int(b): r for r, b in enumerate(blocks)}
+        nb = len(blocks)
+        take = torch.as_tensor(blocks, device=DEV)
+        kb = k.view(B, H, nblk, bs, D)[:, :, take].reshape(B, H, nb * bs, D)
+        vb = v.view(B, H, nblk, bs, D)[:, :, take].reshape(B, H, nb * bs, D)
+        qb = torch.zeros(B, H, nb, bs, D, dtype=q.dtype, device=DEV)
+        qb[:, :, rank[i]] = q.view(B, H, nblk, bs, D)[:, :, i]
+        smini = np.zeros((B, 1, nb, srow.size), np.int64)
+        smini[0, 0, rank[i]] = [rank[int(j)] for j in srow]
+        so, _ = oattn.fwd(np64(qb.reshape(B, H, nb * bs, D)), np64(kb), np64(vb), smini, "slot_causal",
+                          rows=[rank[i]])
+        ex, _ = _check(f"config 5 o block {i} (oracle)", o[:, :, i * bs:(i + 1) * bs].cpu(), so, "bf16")
+        worst = max(worst, ex)
+    _say(f"config 5 o over {len(rows)} sampled blocks: worst max_abs={worst:.3e}")

@@ -37,7 +37,10 @@ def test_config1_shape_mean_pooled_selection(dtype):
     assert_close(o, ro, dtype, "o")
     fin = np.isfinite(rl)
     assert np.array_equal(fin, np.isfinite(lse))
-    assert np.max(np.abs(lse[fin] - rl[fin])) < (1e-4 if dtype == "f32" else 2e-2)
+    # the row normalisers are fp32 sums of the unrounded exponentials in every dtype
+    lerr = float(np.max(np.abs(lse[fin] - rl[fin])))
+    print(f"  lse ({dtype}): max_abs={lerr:.2e}", flush=True)
+    assert lerr < 1e-4
 
 
 def test_config2_shape_gate_bias():
