@@ -96,6 +96,9 @@ enum { KIND_FULL = 0, KIND_DIAG = 1, KIND_ABS = 2, KIND_PAD = 3 };
 #ifndef FBSA_SEG_CHUNKS
 #define FBSA_SEG_CHUNKS 512
 #endif
+#ifndef FBSA_DKDV_UNROLL
+#define FBSA_DKDV_UNROLL 1
+#endif
 #ifndef FBSA_DKDV_LDS_BUDGET
 #define FBSA_DKDV_LDS_BUDGET 40960
 #endif
@@ -813,6 +816,9 @@ template <typename T, int BS, int D> constexpr int dkdv_minwg() {
 #ifndef FBSA_DKDV_PIPE_LDS_BUDGET
 #define FBSA_DKDV_PIPE_LDS_BUDGET 132096
 #endif
+// the one-role chunk loop unrolled by the ring depth (16-bit, d <= 64, every
+// stage offset within a 16-bit LDS instruction offset)
+template <typename T, int BS, int D> constexpr bool dkdv_unrolled();
 template <typename T, int BS, int D> constexpr bool dkdv_pipe() {
   return dkdv_roles<T, D>() == 2 && dkdv_rows<T, BS, D>() >= 128 && FBSA_DKDV_PIPE;
 }
@@ -824,6 +830,10 @@ using DkdvCfg = BwdCfg<T, BS, D,
                            ? FBSA_DKDV_HEAVY_LDS_BUDGET / dkdv_minwg<T, BS, D>()
                            : FBSA_DKDV_LDS_BUDGET,
                        1, dkdv_rows<T, BS, D>()>;
+template <typename T, int BS, int D> constexpr bool dkdv_unrolled() {
+  return sizeof(T) == 2 && D <= 64 && dkdv_roles<T, D>() == 1 && DkdvCfg<T, BS, D>::KC >= 64 &&
+         DkdvCfg<T, BS, D>::NSTAGE * DkdvCfg<T, BS, D>::STAGE_BYTES <= 60000 && FBSA_DKDV_UNROLL;
+}
 
 // Latency bound (each chunk is a short chain of LDS reads, MFMAs and
 // exponentials), so occupancy decides: for bs 64 with 16-bit d <= 64 the
@@ -1109,6 +1119,73 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 
 
       int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
+      if constexpr (dkdv_unrolled<T, BS, D>()) {
+        // one role at 16-bit d <= 64: the chunk loop unrolled by the ring depth,
+        // each copy reading a fixed stage, so every LDS operand address is a
+        // loop-invariant per-lane base plus an instruction offset (no address
+        // arithmetic per chunk); otherwise the same steps as the loop below
+        int c = 0;
+        while (c < nchunks) {
+          static_for<C::NSTAGE>([&](auto SC) {
+            constexpr int S = decltype(SC)::value;
+            if (c >= nchunks) return;
+            const int ahead = nchunks - 1 - c;
+            wait_ring<C::LPT + 1>(ahead < C::NSTAGE - 2 ? ahead : C::NSTAGE - 2);
+            lds_barrier();
+            if (c + C::NSTAGE - 1 < nchunks) issue();
+            const int4 meta = s_meta[cx];
+            const int ch = cch;
+            const int kind = meta.y;
+            const float gt = __int_as_float(meta.z);
+            const int64_t i = meta.x;
+            if (++cch == C::NCH) {
+              cch = 0;
+              if (++cg == a.grp) { cg = 0; ++cx; }
+            }
+            int tmin = -(1 << 30);
+            bool kok = true;
+            if (kind == KIND_DIAG) tmin = u;
+            else if (kind == KIND_PAD) kok = keyok;
+            else if (kind == KIND_ABS) {
+              const int64_t tm = (int64_t)u - (i - j) * BS;
+              tmin = (int)(tm < -(1 << 30) ? -(1 << 30) : tm);
+              kok = keyok;
+            }
+            tmin -= ch * C::KC + 4 * g;  // compare against 16m + r
+            static_for<C::KC / HR>([&](auto HC) {
+              constexpr int h = decltype(HC)::value;
+              constexpr int QOFF = S * C::STAGE_BYTES + h * HR * C::CPR * 16, DOFF = QOFF + C::TILE_BYTES;
+              const float2 *Mh = (const float2 *)(stages + S * C::STAGE_BYTES + 2 * C::TILE_BYTES) + h * HR;
+              const int th = tmin - h * HR;
+              f32x4 sacc[HR / 16], dpacc[HR / 16];
+              mm_rows_frag<T, D, HR / 16, 0, QOFF>(stages, kf, sacc, g, p);   // S: query 16m+4g+r, key u
+              mm_rows_frag<T, D, HR / 16, 0, DOFF>(stages, vf, dpacc, g, p);  // dP
+              float pp[HR / 16][4], ds[HR / 16][4];
+#pragma unroll
+              for (int m = 0; m < HR / 16; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float2 ms = Mh[16 * m + 4 * g + r];
+                  const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                  pp[m][r] = ev;
+                  ds[m][r] = ev * (dpacc[m][r] - ms.y);
+                }
+              if (kind != KIND_FULL) {
+#pragma unroll
+                for (int m = 0; m < HR / 16; ++m)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    if (!(kok && (16 * m + r >= th))) { pp[m][r] = 0.f; ds[m][r] = 0.f; }
+              }
+              constexpr bool SP = decltype(SPC)::value;
+              mm_tr_acc<T, D, HR, 0, SP, 1, DOFF>(stages, pp, dvacc, g, p);  // dV^T += dO^T P
+              mm_tr_acc<T, D, HR, 0, SP, 1, QOFF>(stages, ds, dkacc, g, p);  // dK^T += Q^T dS
+            });
+            ++c;
+          });
+        }
+        continue;
+      }
       for (int c = 0; c < nchunks; ++c) {
         // stage c has landed for this wave (LPT + 1 loads per stage; up to NSTAGE - 2 later
         // stages may still be in flight); after the barrier every wave's part has landed and

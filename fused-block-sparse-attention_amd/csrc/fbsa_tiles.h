@@ -38,7 +38,11 @@ template <typename T, int D> struct RowFrag {
 // W > 0 (16-bit types): the tile reads are issued as asm in a sliding window of
 // W outstanding reads, each MFMA waiting only for its own (LDS reads complete
 // in order); W = 0 leaves the schedule to the compiler.
-template <typename T, int D, int NM, int W = 0>
+// TOFF (both products): a compile-time byte offset of the tile from `tile`,
+// carried in the LDS instructions' offset fields (a loop over ring stages
+// unrolled by the stage count passes the ring base, so the per-lane bases stay
+// loop-invariant and no per-chunk address arithmetic remains).
+template <typename T, int D, int NM, int W = 0, int TOFF = 0>
 __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
   if constexpr (sizeof(T) == 2) {
@@ -51,7 +55,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
       s16x8 x[NK];
       auto rd = [&](auto K) {
         constexpr int k = decltype(K)::value, m = k / KS, ks = k % KS;
-        x[k] = lds_read_b128_at<(ks / 4) * 256 + m * 256 * CPR>(kb[ks % 4]);
+        x[k] = lds_read_b128_at<TOFF + (ks / 4) * 256 + m * 256 * CPR>(kb[ks % 4]);
       };
       static_for<(W < NK ? W : NK)>(rd);
       static_for<NK>([&](auto K) {
@@ -72,7 +76,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
         acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const s16x8 x = *(const s16x8 *)(kb[ks % 4] + (ks / 4) * 256 + m * 256 * CPR);
+          const s16x8 x = *(const s16x8 *)(kb[ks % 4] + TOFF + (ks / 4) * 256 + m * 256 * CPR);
           acc[m] = Mfma16<T>::run(x, fr.h[ks], acc[m]);
         }
       }
@@ -85,7 +89,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
     const int row = 16 * m + p;
 #pragma unroll
     for (int ks = 0; ks < D / 4; ++ks) {
-      const float x = *(const float *)(tile + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
+      const float x = *(const float *)(tile + TOFF + (row * CPR + (ks ^ swz(row, CPR))) * 16 + g * 4);
       acc[m] = mfma_f32_16x16x4(x, fr.f[ks], acc[m]);
       if constexpr (D >= 256) if (ks % 16 == 15) asm volatile("" ::: "memory");  // at most 16 loads ahead
     }
@@ -101,7 +105,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
 // (pack8_split), two MFMAs per read, so the product carries x to ~2^-17
 // relative instead of one 16-bit rounding. NX = 2: a second operand x2
 // (plain 16-bit rounding) is accumulated into acc2 from the same tile reads.
-template <typename T, int D, int KC, int TW = 0, bool SPLIT = false, int NX = 1>
+template <typename T, int D, int KC, int TW = 0, bool SPLIT = false, int NX = 1, int TOFF = 0>
 __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC / 16][4], f32x4 *acc, int g, int p,
                                           const float (*x2)[4] = nullptr, f32x4 *acc2 = nullptr) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
@@ -161,8 +165,8 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
         constexpr int t = decltype(TT)::value;
         static_for<KC / 32>([&](auto K2) {
           constexpr int k2 = decltype(K2)::value, off = (t / 8) * 256 + k2 * 512 * CPR;
-          lo[t][k2] = lds_read_tr16_at<off>(vb[t % 8]);
-          hi[t][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[t % 8]);
+          lo[t][k2] = lds_read_tr16_at<TOFF + off>(vb[t % 8]);
+          hi[t][k2] = lds_read_tr16_at<TOFF + off + 256 * CPR>(vb[t % 8]);
         });
       };
       static_for<W>(rd);
@@ -198,8 +202,8 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
           static_for<KC / 32>([&](auto K2) {
             constexpr int k2 = decltype(K2)::value, off = k2 * 512 * CPR;
             // tile t0 + tt: lane base vb[tt] (t0 is a multiple of 8) plus (t0 / 8) * 256
-            lo[tt][k2] = lds_read_tr16_at<off>(vb[tt] + (t0 / 8) * 256);
-            hi[tt][k2] = lds_read_tr16_at<off + 256 * CPR>(vb[tt] + (t0 / 8) * 256);
+            lo[tt][k2] = lds_read_tr16_at<TOFF + off>(vb[tt] + (t0 / 8) * 256);
+            hi[tt][k2] = lds_read_tr16_at<TOFF + off + 256 * CPR>(vb[tt] + (t0 / 8) * 256);
           });
         });
         lds_wait_all();
@@ -233,7 +237,7 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * m + 4 * g + r;
-          const float a = *(const float *)(tile + (row * CPR + ((4 * t + (p >> 2)) ^ swz(row, CPR))) * 16 + (p & 3) * 4);
+          const float a = *(const float *)(tile + TOFF + (row * CPR + ((4 * t + (p >> 2)) ^ swz(row, CPR))) * 16 + (p & 3) * 4);
           acc[t] = mfma_f32_16x16x4(a, x[m][r], acc[t]);
           if constexpr (NX == 2) acc2[t] = mfma_f32_16x16x4(a, x2[m][r], acc2[t]);
         }
@@ -258,7 +262,7 @@ __device__ __forceinline__ void mm_tr_acc(const char *tile, const float (&x)[KC 
     for (int t = 0; t < D / 16; ++t) {
       const int cb = 2 * t + ((p & 3) >> 1);
       const int ra = 4 * g + (p >> 2);
-      a[t] = lds_read_tr16(tile + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
+      a[t] = lds_read_tr16(tile + TOFF + (ra * CPR + (cb ^ swz(ra, CPR))) * 16 + (p & 1) * 8);
     }
     lds_wait_all();
 #pragma unroll
