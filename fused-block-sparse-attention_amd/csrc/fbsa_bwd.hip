@@ -3,7 +3,9 @@
 // Four stages, none of them with floating-point atomics (results are bitwise
 // repeatable):
 //   1. prep_kernel     per query row: delta = sum_d dO*O and lse*log2(e)
-//                      (rowstat); with an output gate also dO*sigmoid(g) and
+//                      (rowstat, both stored negated so that they enter the
+//                      exponent and the dP accumulators as they are); with an
+//                      output gate also dO*sigmoid(g) and
 //                      the gate gradient dO*O*(1 - sigmoid(g)).
 //   2. keys_kernel + stable radix sort (rocPRIM) + seg_off_kernel
 //                      the block-transposed index: for each (b, hsel, key
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
   if (row < a.rows && c == 0) {
     const float l = a.lse[row];
-    a.rowstat[row] = make_float2(l == -INFINITY ? INFINITY : l * kLog2e, acc);
+    a.rowstat[row] = make_float2(l == -INFINITY ? -INFINITY : -l * kLog2e, -acc);  // negated: (-lse log2 e, -delta)
   }
 }
 
@@ -446,7 +448,7 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 // ----------------------------------------------------------------- stages 3, 4
 struct BwdArgs {
   const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
-  float2 *rowstat;  // (lse * log2 e, delta); dq_kernel replaces delta by sum P dP (16-bit types)
+  float2 *rowstat;  // negated (-lse * log2 e, -delta); dq_kernel replaces delta by sum P dP (16-bit types)
   const int32_t *sel;
   const float *gate;
   void *dq, *dk, *dv;
@@ -514,7 +516,10 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   constexpr bool CORR = EXACT && D <= FBSA_DQ_CORR_DMAX;
   constexpr bool DQSPLIT = EXACT && FBSA_DQ_SPLIT;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, p = lane & 15;
+  // (the wave index in a scalar register: every per-wave LDS and copy address is scalar
+  // work; not with the gate gradient, whose scalar registers are short)
+  const int tid = threadIdx.x, w = DG ? tid >> 6 : __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63,
+            g = lane >> 4, p = lane & 15;
   const int64_t total = a.B * a.Hq * a.nblk;
   // (32-bit division: launch indices are below 2^31)
   uint32_t t = (uint32_t)xcd_remap(blockIdx.x, total);
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   qf.load((const T *)a.q + b * a.sq[0] + hq * a.sq[1] + qpos * a.sq[2], g);
   df.load((const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1] + qpos * a.sdo[2], g);
   const float2 rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
-  const float lse2 = rs.x, delta = rs.y;
+  const float lse2 = -rs.x, delta = -rs.y;  // stored negated
   __syncthreads();
   const int nv = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
@@ -618,6 +623,13 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
                                    (const char *)(vbase + row0 * a.sv[2]), w);
   };
 
+  // dP^T accumulators start at -delta (16-bit types without the gate gradient, whose
+  // registers are short: dS = P (dP - delta) is then one product; the others keep
+  // the separate subtraction)
+  constexpr bool DINIT = EXACT && !DG;
+  f32x4 dinit[C::KC / 16];
+#pragma unroll
+  for (int m = 0; m < C::KC / 16; ++m) dinit[m] = f32x4{-delta, -delta, -delta, -delta};
   f32x4 dqacc[D / 16], bacc[CORR ? D / 16 : 1];  // bacc: sum P K (the delta correction)
 #pragma unroll
   for (int mt = 0; mt < D / 16; ++mt) dqacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -663,7 +675,8 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
 
     f32x4 sacc[C::KC / 16], dpacc[C::KC / 16];
     mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Ks, qf, sacc, g, p);   // S^T: key 16m+4g+r, query p
-    mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Vs, df, dpacc, g, p);  // dP^T
+    mm_rows_frag<T, D, C::KC / 16, (D >= 128 ? FBSA_DQ_WIN : 0)>(Vs, df, dpacc, g, p,
+                                                                  DINIT ? dinit : nullptr);  // dP^T (- delta)
 
     const float off = gt - lse2;
     float ds[C::KC / 16][4], pp[C::KC / 16][4];
@@ -673,7 +686,7 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
       for (int r = 0; r < 4; ++r) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, off));
         pp[m][r] = pv;
-        ds[m][r] = pv * (dpacc[m][r] - delta);
+        ds[m][r] = DINIT ? pv * dpacc[m][r] : pv * (dpacc[m][r] - delta);
       }
     // masked keys (key row 16m + r of the chunk valid iff <= lim): a uniform
     // branch, so unmasked chunks (the common case) skip the compares
@@ -724,14 +737,16 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
       mm_tr_acc<T, D, C::KC, (D >= 128 ? FBSA_BWD_TRWIN : 0), DQSPLIT>(Ks, ds, dqacc, g, p);
   }
 
-  // the row's delta as sum P dP (its four lanes' parts); dgate and dQ take the
-  // difference to the prep's delta, dK/dV read the new value from the row stats
+  // the row's delta as sum P dP (its four lanes' parts); with DINIT dacc holds
+  // sum P (dP - delta_prep), which is delta - delta_prep since the row's P sums
+  // to 1 (to fp32 rounding). dgate and dQ take the difference to the prep's
+  // delta, dK/dV read the new delta from the row stats
   float ddl = 0.f;
   if constexpr (EXACT) {
     float dx = dacc + shfl_xor_f(dacc, 16);
     dx += shfl_xor_f(dx, 32);
-    ddl = dx - delta;
-    if (g == 0) a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = dx;
+    ddl = DINIT ? dx : dx - delta;
+    if (g == 0) a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = -(DINIT ? delta + dx : dx);
   }
 
   T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
@@ -1051,7 +1066,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 const float4 pv = xs[m * XS];
                 const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
   #pragma unroll
-                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] - pM[16 * m + 4 * g + r].y);
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] + pM[16 * m + 4 * g + r].y);
               }
               tr_acc(SPC, pQ, x, dvacc);  // dK^T += Q^T dS
             }
@@ -1092,7 +1107,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
               for (int r = 0; r < 4; ++r) {
                 const float2 ms = Ms[16 * m + 4 * g + r];
                 const bool ok = kok && (16 * m + r >= tmin);
-                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
                 asm volatile("" : "+v"(ev));
                 x[m][r] = ok ? ev : 0.f;
               }
@@ -1165,10 +1180,10 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
               for (int m = 0; m < HR / 16; ++m)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float2 ms = Mh[16 * m + 4 * g + r];
-                  const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                  const float2 ms = Mh[16 * m + 4 * g + r];  // (-lse log2 e, -delta)
+                  const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
                   pp[m][r] = ev;
-                  ds[m][r] = ev * (dpacc[m][r] - ms.y);
+                  ds[m][r] = ev * (dpacc[m][r] + ms.y);
                 }
               if (kind != KIND_FULL) {
 #pragma unroll
@@ -1245,7 +1260,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 for (int r = 0; r < 4; ++r) {
                   const float2 ms = Mh[16 * m + 4 * g + r];
                   const bool ok = kok && (16 * m + r >= th);
-                  float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+                  float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
                   asm volatile("" : "+v"(ev));
                   x[m][r] = ok ? ev : 0.f;
                 }
@@ -1261,7 +1276,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 const float4 pv = xs[m * XS];
                 const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
   #pragma unroll
-                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] - Mh[16 * m + 4 * g + r].y);
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] + Mh[16 * m + 4 * g + r].y);
               }
               tr_acc(SPC, Qh, x, dvacc);  // dK^T += Q^T dS
             }
@@ -1279,9 +1294,9 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float2 ms = Mh[16 * m + 4 * g + r];
-              const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt - ms.x : -ms.x));
+              const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
               pp[m][r] = ev;
-              ds[m][r] = ev * (dpacc[m][r] - ms.y);
+              ds[m][r] = ev * (dpacc[m][r] + ms.y);
             }
           if (kind != KIND_FULL) {
   #pragma unroll

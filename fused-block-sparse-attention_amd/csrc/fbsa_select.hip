@@ -391,6 +391,87 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a0, PoolArgs a1
   }
 }
 
+// Token mean of a block with one input head per output head (mean pooling
+// with grp == 1): one block per wave, four per workgroup. DC lanes cover a row
+// (8 elements each), 64 / DC rows at a time; a lane's BS / (64 / DC) row loads
+// are issued back to back, its exact fp64 sums meet by in-wave xor-shuffles,
+// and no LDS or workgroup barrier is involved (the workgroup-per-block kernel
+// leaves three of its four waves idle in this case). The result is the one
+// pool_wave_kernel writes: the block sum rounded once after the exact division
+// by BS, and, when norm is set, the pooled row's sum of squares over
+// d = 0, 1, ... in order. Waves [0, nb0) pool a0, waves [nb0, nbt) pool a1.
+template <typename T, int DC, int BS>
+__global__ __launch_bounds__(256) void pool_mean1_kernel(PoolArgs a0, PoolArgs a1, int64_t nb0, int64_t nbt) {
+  constexpr int TLW = 64 / DC;
+  constexpr int RPL = BS >= TLW ? BS / TLW : 1;  // rows per lane
+  const int lane = threadIdx.x & 63, c = lane % DC, tl = lane / DC;
+  const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wv >= nbt) return;  // wave-uniform
+  const bool second = wv >= nb0;
+  const PoolArgs a = second ? a1 : a0;
+  const int64_t blk = second ? wv - nb0 : wv;
+  const int64_t i = blk % a.nblk;
+  const int64_t ho = (blk / a.nblk) % a.Ho;
+  const int64_t b = blk / (a.nblk * a.Ho);
+  const int64_t nval = a.l_valid - i * BS < BS ? a.l_valid - i * BS : BS;  // valid tokens (>= 1)
+  const T *base = (const T *)a.x + b * a.sx[0] + ho * a.sx[1] + i * BS * a.sx[2] + 8 * c;
+  Raw8<T> raw[RPL];
+#pragma unroll
+  for (int n = 0; n < RPL; ++n) {
+    const int t = tl + n * TLW;
+    const int tc = t < nval ? t : (int)nval - 1;  // rows past l_valid: a clamped address, counted as 0
+    raw[n] = load_raw8<T>(base + tc * a.sx[2]);
+  }
+  double acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0;
+#pragma unroll
+  for (int n = 0; n < RPL; ++n) {
+    const int t = tl + n * TLW;
+    const bool ok = t < nval && t < BS;
+    double v[8];
+    decode8<T>(raw[n], v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += ok ? v[e] : 0.0;
+  }
+#pragma unroll
+  for (int off = DC; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+  float yf[8];
+  T y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    yf[e] = round_dt<T>(acc[e] * (1.0 / (double)BS));  // BS is a power of two: the product is the quotient
+    y[e] = (T)yf[e];
+  }
+  if (tl == 0) {
+    T *o = (T *)a.out + ((b * a.Ho + ho) * a.nblk + i) * a.D + 8 * c;
+    if (((uintptr_t)o & 15) == 0) {
+      uint4 u[sizeof(T) / 2];
+      __builtin_memcpy(u, y, sizeof(y));
+#pragma unroll
+      for (int q = 0; q < (int)(sizeof(T) / 2); ++q) ((uint4 *)o)[q] = u[q];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = y[e];
+    }
+  }
+  if (a.norm) {
+    // element 8 cc + e of the pooled row is yf[e] of lane cc; every lane forms
+    // the same ordered sum and lane 0 writes it
+    double ss = 0.0;
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double v = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(yf[e]), cc));
+        ss += v * v;
+      }
+    if (lane == 0) a.norm[(b * a.Ho + ho) * a.norm_pitch + i] = sel_row_norm(ss, a.norm_key != 0);
+  }
+}
+
 // Per-token group mean (bs = 1, MEAN_GRP_THEN_TOK): one thread per 8-element
 // chunk of an output row, the exact fp64 group sum rounded once as in the
 // block kernels (the mean over one token is the identity), coalesced 16-byte
@@ -442,6 +523,10 @@ __global__ __launch_bounds__(256) void pool_grp_kernel(PoolArgs a, int64_t n) {
 template <typename T, int DC, int BS> static void launch_pool_op(const PoolArgs &a, int64_t nwg, hipStream_t s) {
   switch (a.op) {
     case FBSA_POOL_MEAN_TOK_THEN_GRP:
+      if (a.grp == 1) {
+        hipLaunchKernelGGL((pool_mean1_kernel<T, DC, BS>), dim3((unsigned)((nwg + 3) / 4)), dim3(256), 0, s, a, a, nwg, nwg);
+        return;
+      }
       hipLaunchKernelGGL((pool_wave_kernel<T, DC, BS, FBSA_POOL_MEAN_TOK_THEN_GRP>), dim3((unsigned)nwg), dim3(256), 0, s, a,
                          a, nwg);
       return;
@@ -1809,6 +1894,16 @@ template <typename T, int D> static int pooled_pair(const fbsa_pool_desc *dq, co
   a0.norm = nq; a0.norm_pitch = pitch; a0.norm_key = 0;
   a1.norm = nk; a1.norm_pitch = pitch; a1.norm_key = 1;
   const int64_t nwg0 = a0.B * a0.Ho * a0.nblk, nwg1 = a1.B * a1.Ho * a1.nblk;
+  if (a0.grp == 1 && a1.grp == 1) {  // plain token means: one block per wave
+    const dim3 g4((unsigned)((nwg0 + nwg1 + 3) / 4));
+    switch (dq->bs) {
+      case 16: hipLaunchKernelGGL((pool_mean1_kernel<T, DC, 16>), g4, dim3(256), 0, s, a0, a1, nwg0, nwg0 + nwg1); break;
+      case 32: hipLaunchKernelGGL((pool_mean1_kernel<T, DC, 32>), g4, dim3(256), 0, s, a0, a1, nwg0, nwg0 + nwg1); break;
+      case 64: hipLaunchKernelGGL((pool_mean1_kernel<T, DC, 64>), g4, dim3(256), 0, s, a0, a1, nwg0, nwg0 + nwg1); break;
+      default: hipLaunchKernelGGL((pool_mean1_kernel<T, DC, 128>), g4, dim3(256), 0, s, a0, a1, nwg0, nwg0 + nwg1); break;
+    }
+    return hip_check(hipGetLastError(), "pool_mean1_kernel (pair) launch");
+  }
   const dim3 grid((unsigned)(nwg0 + nwg1));
   switch (dq->bs) {
     case 16: hipLaunchKernelGGL((pool_wave_kernel<T, DC, 16, FBSA_POOL_MEAN_TOK_THEN_GRP>), grid, dim3(256), 0, s, a0, a1, nwg0); break;

@@ -42,8 +42,11 @@ template <typename T, int D> struct RowFrag {
 // carried in the LDS instructions' offset fields (a loop over ring stages
 // unrolled by the stage count passes the ring base, so the per-lane bases stay
 // loop-invariant and no per-chunk address arithmetic remains).
+// acc0 (optional): the accumulators' initial values instead of zeros (a
+// rank-1 term such as -delta enters the product at no VALU cost).
 template <typename T, int D, int NM, int W = 0, int TOFF = 0>
-__device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p) {
+__device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, D> &fr, f32x4 *acc, int g, int p,
+                                             const f32x4 *acc0 = nullptr) {
   constexpr int CPR = D * (int)sizeof(T) / 16;
   if constexpr (sizeof(T) == 2) {
     // read (m, ks) at lane base kb[ks % 4] + (ks / 4) * 256 + m * 256 * CPR
@@ -63,7 +66,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
         constexpr int last = k + W - 1 < NK - 1 ? k + W - 1 : NK - 1;  // last read issued so far
         lds_wait_le<(last - k < 15 ? last - k : 15)>();
         lds_ready(x[k]);
-        if constexpr (k % KS == 0) acc[k / KS] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (k % KS == 0) acc[k / KS] = acc0 ? acc0[k / KS] : f32x4{0.f, 0.f, 0.f, 0.f};
         acc[k / KS] = Mfma16<T>::run(x[k], fr.h[k % KS], acc[k / KS]);
         if constexpr (k + W < NK) rd(std::integral_constant<int, k + W>{});
       });
@@ -73,7 +76,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
       for (int l = 0; l < KL; ++l) kb[l] = tile + tile_kbase(l, g, p, CPR);
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[m] = acc0 ? acc0[m] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const s16x8 x = *(const s16x8 *)(kb[ks % 4] + TOFF + (ks / 4) * 256 + m * 256 * CPR);
@@ -85,7 +88,7 @@ __device__ __forceinline__ void mm_rows_frag(const char *tile, const RowFrag<T, 
   }
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
-    acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[m] = acc0 ? acc0[m] : f32x4{0.f, 0.f, 0.f, 0.f};
     const int row = 16 * m + p;
 #pragma unroll
     for (int ks = 0; ks < D / 4; ++ks) {

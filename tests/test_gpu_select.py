@@ -18,10 +18,12 @@ def _say(*a):
 
 
 @pytest.mark.parametrize("dtype,H", [("f32", 4), ("bf16", 4), ("f16", 4),
-                                     ("bf16", 6), ("bf16", 12), ("f16", 13)])
+                                     ("bf16", 6), ("bf16", 12), ("f16", 13),
+                                     ("f32", 1), ("bf16", 1), ("f16", 1)])
 def test_pool_mean_tok_then_heads_exact(dtype, H):
     """Mean over tokens, then over H heads. A wave takes heads w, w + 4, ... and
-    loads two of them together: 6, 12 and 13 heads leave waves with an odd count."""
+    loads two of them together: 6, 12 and 13 heads leave waves with an odd count.
+    One head (a plain token mean) runs one block per wave, four per workgroup."""
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(0)
     B, N, D, bs = 2, 1000, 64, 64                # N % bs != 0: zero-padded tail block
@@ -85,6 +87,8 @@ def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal, engine):
     ("bf16", 1, 4, 4, 4096, 64, 64, 49, 1.0),      # budget past the MFMA engine: pool, pool, select
     ("bf16", 1, 2, 2, 4096, 64, 64, 16, 1e19),     # norms past 1e18: every pair takes the exact path
     ("bf16", 1, 2, 2, 4096, 32, 64, 16, 1e-20),    # norms below 2^-40: likewise
+    ("bf16", 3, 1, 1, 3000, 64, 32, 16, 1.0),      # one head: plain token means, a block per wave
+    ("f16", 1, 1, 1, 4000, 32, 128, 8, 1.0),
 ])
 def test_select_mean_pooled_fused_equals_separate_calls(dtype, B, Hq, Hk, N, D, bs, topk, scale):
     """fbsa_select_mean_pooled (q and k pooled by one launch that also writes the
