@@ -1810,11 +1810,15 @@ static void sel_chunking(int64_t B, int64_t H, int64_t nblk, bool tri, int64_t o
   *nch = (ntiles + c - 1) / c;
 }
 
+// Budgets up to 32: past that the pass-1 bound (the K-th of 64 stream maxima)
+// lets most candidates through and the row buffers are cut over and over
+// (k = 40: 204 against 217 us for the fp64 path over 4096 blocks; k = 48: 759
+// against 239 us), so larger budgets take the fp64 path.
 template <typename T, int D, int MODE> static bool sel_tiled_ok(const SelArgs &a) {
   if constexpr (sizeof(T) != 2 || (D != 32 && D != 64)) return false;
   const int64_t K = a.conv == FBSA_SEL_OWN_FIRST ? (a.topk < a.nblk - 1 ? a.topk : a.nblk - 1)
                                                  : (a.topk < a.nblk ? a.topk : a.nblk);
-  return K >= 1 && K <= 48;
+  return K >= 1 && K <= 32;
 }
 
 template <typename T, int D, int MODE> static int launch_sel(const SelArgs &a, void *ws, hipStream_t s) {
@@ -1963,7 +1967,7 @@ template <typename T, int D> static int pooled_pair(const fbsa_pool_desc *dq, co
 int run_select_mean_pooled(const fbsa_pool_desc *dq, const void *q, void *qp, const fbsa_pool_desc *dk, const void *k,
                            void *kp, const fbsa_select_desc *d, int32_t *sel, float *sel_score, void *ws, hipStream_t s) {
   const int64_t K = d->topk < d->nblk - 1 ? d->topk : d->nblk - 1;
-  const bool fused = ws && d->dtype != FBSA_F32 && (d->D == 32 || d->D == 64) && K >= 1 && K <= 48 &&
+  const bool fused = ws && d->dtype != FBSA_F32 && (d->D == 32 || d->D == 64) && K >= 1 && K <= 32 &&
                      (dq->bs == 16 || dq->bs == 32 || dq->bs == 64 || dq->bs == 128);
   if (!fused) {
     int e = run_pool(dq, q, qp, nullptr, s);

@@ -182,7 +182,7 @@ int fbsa_select_rows(const fbsa_select_desc *d, int64_t row_begin, int64_t row_e
  * fbsa_select with d. dq and dk share dtype, B, L, D, bs, nblk and l_valid,
  * and H/grp equals d->H for both. With a workspace of at least
  * fbsa_select_workspace_bytes(d) bytes and 16-bit operands of dim 32 or 64
- * (top-k budget <= 48), both tensors are pooled by one launch that also writes
+ * (top-k budget <= 32), both tensors are pooled by one launch that also writes
  * the selection's row norms, so the call takes three launches instead of five;
  * otherwise it runs fbsa_pool twice and fbsa_select. qp, kp, sel and sel_score
  * are identical either way. Replaces the pooling of src/ssa_model.py:287-288

@@ -81,7 +81,8 @@ def test_select_mean_pooled_exact(dtype, B, H, N, bs, topk, causal, engine):
 
 @pytest.mark.parametrize("dtype,B,Hq,Hk,N,D,bs,topk,scale", [
     ("bf16", 1, 8, 8, 16384, 64, 64, 16, 1.0),     # config 3's shape, shorter
-    ("bf16", 2, 4, 2, 3000, 64, 32, 48, 1.0),      # ragged tail block, largest fused budget
+    ("bf16", 2, 4, 2, 3000, 64, 32, 32, 1.0),      # ragged tail block, largest fused budget
+    ("bf16", 2, 4, 2, 3000, 64, 32, 48, 1.0),      # past it: pool, pool, fp64 select
     ("f16", 1, 2, 1, 2048, 32, 16, 8, 1.0),
     ("bf16", 1, 2, 2, 4096, 64, 128, 20, 1.0),
     ("bf16", 1, 4, 4, 4096, 64, 64, 49, 1.0),      # budget past the MFMA engine: pool, pool, select
@@ -251,7 +252,8 @@ def test_select_config5_prefix_invariance_and_sampled_rows():
 @pytest.mark.parametrize("D", [32, 64])
 @pytest.mark.parametrize("score", ["dot", "max2", "quest"])
 @pytest.mark.parametrize("conv,causal,topk", [("own_first", True, 16), ("own_first", False, 16),
-                                              ("sorted_sink", True, 16), ("own_first", True, 48)])
+                                              ("sorted_sink", True, 16), ("own_first", True, 32),
+                                              ("own_first", True, 48)])
 @pytest.mark.parametrize("ties,chunk", [(False, 0), (True, 0), (False, 4), (True, 1)])
 def test_select_tiled_modes(dtype, D, score, conv, causal, topk, ties, chunk):
     # The MFMA engine over every score mode / convention / width it takes, with
