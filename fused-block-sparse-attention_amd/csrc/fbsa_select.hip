@@ -1514,52 +1514,6 @@ __global__ __launch_bounds__(256) void select_tiled_kernel(SelArgs a) {
         for (int r = 0; r < 4; ++r) sv |= sr[t][r] ? 1u << (4 * t + r) : 0u;
       sv &= vm;
 
-      // Fast path: every survivor of the tile appended at once. A lane's
-      // survivors for its row 4g + r are bits r, r + 4, r + 8, r + 12 of sv; the
-      // four per-row counts, packed a byte each (at most 64 per row and group),
-      // take one exclusive prefix sum over the group's 16 lanes, which gives each
-      // survivor its slot. Taken when no row of the wave would pass the buffer's
-      // capacity (almost always: a row keeps about K entries per chunk).
-      {
-        uint32_t cnt4 = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cnt4 |= (uint32_t)__builtin_popcount(sv & (0x1111u << r)) << (8 * r);
-        uint32_t inc = cnt4;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-          const uint32_t y = (uint32_t)__shfl_up((int)inc, d, 16);
-          if (p >= d) inc += y;
-        }
-        const uint32_t tot4 = (uint32_t)__shfl((int)inc, 15, 16), pre4 = inc - cnt4;
-        bool fits = true;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) fits = fits && rcl[r] + (int)((tot4 >> (8 * r)) & 0xFF) <= C::CAP;
-        if (__ballot(!fits) == 0) {  // wave-uniform
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t mrow = sv & (0x1111u << r);
-            const int base = rcl[r] + (int)((pre4 >> (8 * r)) & 0xFF);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int bit = 4 * t + r;
-              if ((mrow >> bit) & 1u) {
-                uint32_t hb = 0;
-                if constexpr (MODE == FBSA_SCORE_DOT) {
-                  hb = __float_as_uint(acc[0][t][r]);
-                } else if constexpr (MODE == FBSA_SCORE_MAX2) {
-                  const float h0 = acc[0][t][r], h1 = acc[1][t][r];
-                  hb = __float_as_uint(h0 != h0 || h1 != h1 ? __builtin_nanf("") : fmaxf(h0, h1));
-                }
-                const int slot = base + __builtin_popcount(mrow & ((1u << bit) - 1u));
-                buf[16 * w + 4 * g + r][slot] = ((uint64_t)hb << 32) | (uint32_t)(j0 + 16 * t + p + 1);
-              }
-            }
-            rcl[r] += (int)((tot4 >> (8 * r)) & 0xFF);
-          }
-          return;
-        }
-      }
-
       // survivors, one per lane per round, appended as pending entries; the
       // slots come from ballots (rows of a group only receive entries from
       // that group's 16 lanes), the counts live in registers
