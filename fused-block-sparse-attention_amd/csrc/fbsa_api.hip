@@ -362,11 +362,14 @@ size_t fbsa_bwd_workspace_bytes(const fbsa_attn_desc *d) {
   return lay.total;
 }
 
-int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, const float *lse, const void *out_gate,
-                  void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
-  BwdLayout lay;
-  int e = check_bwd(d, "fbsa_bwd_prep", &lay, workspace, workspace_bytes);
-  if (e) return e;
+}  // extern "C"
+
+namespace fbsa {
+
+// Argument checks of the prep and dQ stages (after check_bwd), shared by the
+// stage entry points and fbsa_bwd.
+static int check_prep_args(const fbsa_attn_desc *d, const void *o, const void *dout, const float *lse,
+                           const void *out_gate, const void *dout_gate) {
   const bool og = (d->flags & FBSA_FLAG_OUT_GATE) != 0;
   if (og != (out_gate != nullptr) || og != (dout_gate != nullptr))
     return fail(FBSA_EINVAL, "fbsa_bwd_prep: out_gate and dout_gate must be given exactly when FBSA_FLAG_OUT_GATE is set");
@@ -378,6 +381,35 @@ int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, cons
       return fail(FBSA_EINVAL, "fbsa_bwd_prep: dout stride[%d] must be a non-negative multiple of 16 bytes", x);
   if (og && (!aligned(out_gate, es) || !aligned(dout_gate, 16)))
     return fail(FBSA_EINVAL, "fbsa_bwd_prep: out_gate / dout_gate misaligned");
+  return FBSA_OK;
+}
+
+static int check_dq_args(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *dout,
+                         const int32_t *sel, const float *gate, void *dq, float *dgate) {
+  int e = check_qkv(q, k, v, "fbsa_bwd_dq");
+  if (!e) e = check_dout(d, dout, "fbsa_bwd_dq");
+  if (e) return e;
+  if ((e = check_dense(d, sel, gate, "fbsa_bwd_dq"))) return e;
+  if ((d->flags & FBSA_FLAG_DENSE) && dgate) return fail(FBSA_EINVAL, "fbsa_bwd_dq: FBSA_FLAG_DENSE has no gate gradient");
+  if (dgate && d->dtype != FBSA_F32 && !(d->flags & FBSA_FLAG_DGATE))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dq: a 16-bit gate gradient needs FBSA_FLAG_DGATE in the descriptor "
+                             "(the workspace then holds the per-row slot masses)");
+  if ((sel && !aligned(sel, 4)) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
+    return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned");
+  if (!dq || !aligned(dq, 16)) return fail(FBSA_EINVAL, "fbsa_bwd_dq: dq must be non-null and 16-byte aligned");
+  return FBSA_OK;
+}
+
+}  // namespace fbsa
+
+extern "C" {
+
+int fbsa_bwd_prep(const fbsa_attn_desc *d, const void *o, const void *dout, const float *lse, const void *out_gate,
+                  void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_bwd_prep", &lay, workspace, workspace_bytes);
+  if (!e) e = check_prep_args(d, o, dout, lse, out_gate, dout_gate);
+  if (e) return e;
   return run_bwd_prep(d, lay, o, dout, lse, out_gate, dout_gate, (char *)workspace, (hipStream_t)stream);
 }
 
@@ -396,17 +428,8 @@ int fbsa_bwd_dq(const fbsa_attn_desc *d, const void *q, const void *k, const voi
                 void *stream) {
   BwdLayout lay;
   int e = check_bwd(d, "fbsa_bwd_dq", &lay, workspace, workspace_bytes);
-  if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dq");
-  if (!e) e = check_dout(d, dout, "fbsa_bwd_dq");
+  if (!e) e = check_dq_args(d, q, k, v, dout, sel, gate, dq, dgate);
   if (e) return e;
-  if ((e = check_dense(d, sel, gate, "fbsa_bwd_dq"))) return e;
-  if ((d->flags & FBSA_FLAG_DENSE) && dgate) return fail(FBSA_EINVAL, "fbsa_bwd_dq: FBSA_FLAG_DENSE has no gate gradient");
-  if (dgate && d->dtype != FBSA_F32 && !(d->flags & FBSA_FLAG_DGATE))
-    return fail(FBSA_EINVAL, "fbsa_bwd_dq: a 16-bit gate gradient needs FBSA_FLAG_DGATE in the descriptor "
-                             "(the workspace then holds the per-row slot masses)");
-  if ((sel && !aligned(sel, 4)) || (gate && !aligned(gate, 4)) || (dgate && !aligned(dgate, 4)))
-    return fail(FBSA_EINVAL, "fbsa_bwd_dq: sel/gate/dgate must be 4-byte aligned");
-  if (!dq || !aligned(dq, 16)) return fail(FBSA_EINVAL, "fbsa_bwd_dq: dq must be non-null and 16-byte aligned");
   return run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, (char *)workspace, (hipStream_t)stream);
 }
 
@@ -427,9 +450,22 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
 int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o, const void *dout,
              const float *lse, const int32_t *sel, const float *gate, const void *out_gate, void *dq, void *dk,
              void *dv, float *dgate, void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
-  int e = fbsa_bwd_prep(d, o, dout, lse, out_gate, dout_gate, workspace, workspace_bytes, stream);
-  if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
-  if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);
+  // 16-bit types without an output gate: the prep stage only forms the row
+  // statistics, which the dQ stage then forms itself (bit for bit the same),
+  // saving the prep's pass over O and dO
+  BwdLayout lay;
+  int e = check_bwd(d, "fbsa_bwd", &lay, workspace, workspace_bytes);
+  if (e) return e;
+  if ((d->flags & FBSA_FLAG_OUT_GATE) || d->dtype == FBSA_F32) {
+    e = fbsa_bwd_prep(d, o, dout, lse, out_gate, dout_gate, workspace, workspace_bytes, stream);
+    if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
+    if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);
+  } else {
+    e = check_prep_args(d, o, dout, lse, out_gate, dout_gate);
+    if (!e) e = check_dq_args(d, q, k, v, dout, sel, gate, dq, dgate);
+    if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
+    if (!e) e = run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, (char *)workspace, (hipStream_t)stream, o, lse);
+  }
   if (!e) e = fbsa_bwd_dkdv(d, q, k, v, dout, gate, dk, dv, workspace, workspace_bytes, stream);
   return e;
 }

@@ -449,6 +449,11 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 struct BwdArgs {
   const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
   float2 *rowstat;  // negated (-lse * log2 e, -delta); dq_kernel replaces delta by sum P dP (16-bit types)
+  // o, lse (16-bit types, no output gate; else null): dq_kernel forms the row
+  // statistics itself (the prep stage is skipped) and writes both to rowstat
+  const void *o;
+  const float *lse;
+  int64_t so[3];
   const int32_t *sel;
   const float *gate;
   void *dq, *dk, *dv;
@@ -595,8 +600,18 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   RowFrag<T, D> qf, df;
   qf.load((const T *)a.q + b * a.sq[0] + hq * a.sq[1] + qpos * a.sq[2], g);
   df.load((const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1] + qpos * a.sdo[2], g);
-  const float2 rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
-  const float lse2 = -rs.x, delta = -rs.y;  // stored negated
+  // the row statistics: from the prep stage, or (fused) formed here exactly as
+  // prep_kernel forms them (below, once the ring's first loads are in flight)
+  const bool fused = EXACT && a.o != nullptr;  // uniform
+  RowFrag<T, D> of;
+  float lraw = 0.f;
+  float2 rs = make_float2(0.f, 0.f);
+  if (fused) {
+    of.load((const T *)a.o + b * a.so[0] + hq * a.so[1] + qpos * a.so[2], g);
+    lraw = a.lse[(b * a.Hq + hq) * a.L + qpos];
+  } else {
+    rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
+  }
   __syncthreads();
   const int nv = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
   const int nchunks = nv * C::NCH;
@@ -627,9 +642,6 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   // registers are short: dS = P (dP - delta) is then one product; the others keep
   // the separate subtraction)
   constexpr bool DINIT = EXACT && !DG;
-  f32x4 dinit[C::KC / 16];
-#pragma unroll
-  for (int m = 0; m < C::KC / 16; ++m) dinit[m] = f32x4{-delta, -delta, -delta, -delta};
   f32x4 dqacc[D / 16], bacc[CORR ? D / 16 : 1];  // bacc: sum P K (the delta correction)
 #pragma unroll
   for (int mt = 0; mt < D / 16; ++mt) dqacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -650,6 +662,34 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   // inside the ring loop, where its own waits would also drain the prefetch
   wait_vmcnt<0>();
 
+  // fused row statistics: per 8-element chunk c = 4 ks + g an fma chain over
+  // dO*O from 0, then the chunks' pairwise tree c + c ^ m for m = D/16 .. 1 (the
+  // lane's own chunks first, then across the lanes g), as prep_kernel sums them
+  float lse2 = -rs.x, delta = -rs.y;  // stored negated
+  if constexpr (EXACT) if (fused) {
+    constexpr int KS = D / 32;
+    float cs[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const s16x8 ov = of.h[ks], dv = df.h[ks];
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        acc = __builtin_fmaf(half_to_f32<T>((uint32_t)(uint16_t)ov[e]), half_to_f32<T>((uint32_t)(uint16_t)dv[e]), acc);
+      cs[ks] = acc;
+    }
+#pragma unroll
+    for (int m = KS / 2; m >= 1; m >>= 1)
+#pragma unroll
+      for (int ks = 0; ks < m; ++ks) cs[ks] += cs[ks + m];
+    float dsum = cs[0] + shfl_xor_f(cs[0], 32);  // chunk pairs c, c ^ 2 (lanes g, g ^ 2)
+    dsum += shfl_xor_f(dsum, 16);                 // c, c ^ 1
+    lse2 = lraw == -INFINITY ? INFINITY : lraw * kLog2e;
+    delta = dsum;
+  }
+  f32x4 dinit[C::KC / 16];
+#pragma unroll
+  for (int m = 0; m < C::KC / 16; ++m) dinit[m] = f32x4{-delta, -delta, -delta, -delta};
 
   for (int c = 0; c < nchunks; ++c) {
     // stage c has landed for this wave (up to NSTAGE - 2 later stages may be in flight);
@@ -746,7 +786,11 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
     float dx = dacc + shfl_xor_f(dacc, 16);
     dx += shfl_xor_f(dx, 32);
     ddl = DINIT ? dx : dx - delta;
-    if (g == 0) a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = -(DINIT ? delta + dx : dx);
+    const float dnew = DINIT ? delta + dx : dx;
+    if (g == 0) {
+      if (fused) a.rowstat[(b * a.Hq + hq) * a.L + qpos] = make_float2(lse2 == INFINITY ? -INFINITY : -lse2, -dnew);
+      else a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = -dnew;
+    }
   }
 
   T *dqrow = (T *)a.dq + ((b * a.Hq + hq) * a.L + qpos) * D;
@@ -1490,6 +1534,8 @@ __global__ __launch_bounds__(256) void dgate_reduce_kernel(const float *part, fl
 
 static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, BwdArgs &a, const void *dout) {
   a.wi_slot = nullptr; a.xtab = nullptr; a.seg_tot = nullptr; a.partials = nullptr;
+  a.o = nullptr; a.lse = nullptr;
+  for (int x = 0; x < 3; ++x) a.so[x] = d->so[x];
   a.seg_entries = a.seg_entries_xub = 0;
   a.B = d->B; a.Hq = d->Hq; a.Hkv = d->Hkv; a.L = d->L; a.nblk = d->nblk; a.kk = d->kk; a.hsel = d->hsel;
   a.l_valid = d->l_valid;
@@ -1584,9 +1630,10 @@ static int bwd_dispatch(const fbsa_attn_desc *d, const BwdArgs &a, bool dq, hipS
 
 int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
                const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate, char *ws,
-               hipStream_t s) {
+               hipStream_t s, const void *o, const float *lse) {
   BwdArgs a;
   fill_bwd(d, lay, ws, a, dout);
+  a.o = o; a.lse = lse;
   a.q = q; a.k = k; a.v = v; a.sel = sel; a.gate = gate; a.dq = dq; a.dk = a.dv = nullptr;
   a.dgate_part = dgate ? (float *)(ws + lay.dgate_part) : nullptr;
   a.pmass = (float *)(ws + lay.pmass);

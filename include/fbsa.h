@@ -303,7 +303,10 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
 
 /* All four stages in order. lse is the forward's (fbsa_fwd) output; o is the
  * forward output (gated when out_gate != NULL). dgate and dout_gate are
- * nullable. Replaces _bsattn_bwd / bsattn_backward
+ * nullable. For 16-bit types without an output gate the prep stage's only
+ * output is the row statistics, and the dQ stage forms them itself from o and
+ * lse (the same values, summed in the same order), so no separate pass over o
+ * and dout runs. Replaces _bsattn_bwd / bsattn_backward
  * (src/triton_kernel.py:77-181, 210-234) and the autograd of the gather path
  * (src/ssa_model.py:57-90). */
 int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o,
