@@ -450,13 +450,14 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
 int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o, const void *dout,
              const float *lse, const int32_t *sel, const float *gate, const void *out_gate, void *dq, void *dk,
              void *dv, float *dgate, void *dout_gate, void *workspace, size_t workspace_bytes, void *stream) {
-  // 16-bit types without an output gate: the prep stage only forms the row
-  // statistics, which the dQ stage then forms itself (bit for bit the same),
-  // saving the prep's pass over O and dO
+  // bf16 without an output gate: the prep stage only forms the row statistics,
+  // which the dQ stage then forms itself (bit for bit the same), saving the
+  // prep's pass over O and dO (fp16 keeps the prep: its sums were not
+  // bit-identical between the two kernels' code)
   BwdLayout lay;
   int e = check_bwd(d, "fbsa_bwd", &lay, workspace, workspace_bytes);
   if (e) return e;
-  if ((d->flags & FBSA_FLAG_OUT_GATE) || d->dtype == FBSA_F32) {
+  if ((d->flags & FBSA_FLAG_OUT_GATE) || d->dtype != FBSA_BF16) {
     e = fbsa_bwd_prep(d, o, dout, lse, out_gate, dout_gate, workspace, workspace_bytes, stream);
     if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
     if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);

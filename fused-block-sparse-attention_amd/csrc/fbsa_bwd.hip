@@ -449,7 +449,7 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 struct BwdArgs {
   const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
   float2 *rowstat;  // negated (-lse * log2 e, -delta); dq_kernel replaces delta by sum P dP (16-bit types)
-  // o, lse (16-bit types, no output gate; else null): dq_kernel forms the row
+  // o, lse (bf16, no output gate; else null): dq_kernel forms the row
   // statistics itself (the prep stage is skipped) and writes both to rowstat
   const void *o;
   const float *lse;
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   df.load((const T *)a.dout + b * a.sdo[0] + hq * a.sdo[1] + qpos * a.sdo[2], g);
   // the row statistics: from the prep stage, or (fused) formed here exactly as
   // prep_kernel forms them (below, once the ring's first loads are in flight)
-  const bool fused = EXACT && a.o != nullptr;  // uniform
+  const bool fused = __is_same(T, bf16) && a.o != nullptr;  // uniform
   RowFrag<T, D> of;
   float lraw = 0.f;
   float2 rs = make_float2(0.f, 0.f);
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
   // dO*O from 0, then the chunks' pairwise tree c + c ^ m for m = D/16 .. 1 (the
   // lane's own chunks first, then across the lanes g), as prep_kernel sums them
   float lse2 = -rs.x, delta = -rs.y;  // stored negated
-  if constexpr (EXACT) if (fused) {
+  if constexpr (__is_same(T, bf16)) if (fused) {
     constexpr int KS = D / 32;
     float cs[KS];
 #pragma unroll

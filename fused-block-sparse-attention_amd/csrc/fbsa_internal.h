@@ -66,7 +66,7 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay);
 int run_bwd_prep(const fbsa_attn_desc *d, const BwdLayout &lay, const void *o, const void *dout, const float *lse,
                  const void *out_gate, void *dout_gate, char *ws, hipStream_t s);
 int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int32_t *sel, char *ws, hipStream_t s);
-// o, lse non-null (16-bit types, no output gate): the dQ stage forms the row
+// o, lse non-null (bf16, no output gate): the dQ stage forms the row
 // statistics itself, in place of the prep stage
 int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
                const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate, char *ws,

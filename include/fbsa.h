@@ -303,7 +303,7 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
 
 /* All four stages in order. lse is the forward's (fbsa_fwd) output; o is the
  * forward output (gated when out_gate != NULL). dgate and dout_gate are
- * nullable. For 16-bit types without an output gate the prep stage's only
+ * nullable. For bf16 without an output gate the prep stage's only
  * output is the row statistics, and the dQ stage forms them itself from o and
  * lse (the same values, summed in the same order), so no separate pass over o
  * and dout runs. Replaces _bsattn_bwd / bsattn_backward
