@@ -384,6 +384,29 @@ static int check_prep_args(const fbsa_attn_desc *d, const void *o, const void *d
   return FBSA_OK;
 }
 
+// A second stream per (host thread, device) for fbsa_bwd's index stage, which
+// only reads sel and so runs beside the dQ stage: created on first use with
+// the default priority, kept for the life of the process. Per thread, so that
+// concurrent calls from other threads (or a capture on one of them) never
+// share it.
+static int side_stream(hipStream_t *out) {
+  constexpr int kMaxDev = 64;
+  thread_local hipStream_t streams[kMaxDev] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_check(e, "fbsa_bwd: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDev) return fail(FBSA_EUNSUPPORTED, "fbsa_bwd: device ordinal %d beyond %d", dev, kMaxDev);
+  if (!streams[dev]) {
+    e = hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      streams[dev] = nullptr;
+      return hip_check(e, "fbsa_bwd: hipStreamCreateWithFlags");
+    }
+  }
+  *out = streams[dev];
+  return FBSA_OK;
+}
+
 static int check_dq_args(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *dout,
                          const int32_t *sel, const float *gate, void *dq, float *dgate) {
   int e = check_qkv(q, k, v, "fbsa_bwd_dq");
@@ -461,13 +484,37 @@ int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
     e = fbsa_bwd_prep(d, o, dout, lse, out_gate, dout_gate, workspace, workspace_bytes, stream);
     if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
     if (!e) e = fbsa_bwd_dq(d, q, k, v, dout, sel, gate, dq, dgate, workspace, workspace_bytes, stream);
-  } else {
-    e = check_prep_args(d, o, dout, lse, out_gate, dout_gate);
-    if (!e) e = check_dq_args(d, q, k, v, dout, sel, gate, dq, dgate);
-    if (!e) e = fbsa_transpose_index(d, sel, workspace, workspace_bytes, stream);
-    if (!e) e = run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, (char *)workspace, (hipStream_t)stream, o, lse);
+    if (!e) e = fbsa_bwd_dkdv(d, q, k, v, dout, gate, dk, dv, workspace, workspace_bytes, stream);
+    return e;
   }
-  if (!e) e = fbsa_bwd_dkdv(d, q, k, v, dout, gate, dk, dv, workspace, workspace_bytes, stream);
+  e = check_prep_args(d, o, dout, lse, out_gate, dout_gate);
+  if (!e) e = check_dq_args(d, q, k, v, dout, sel, gate, dq, dgate);
+  if (!e) e = check_qkv(q, k, v, "fbsa_bwd_dkdv");
+  if (!e && ((d->flags & FBSA_FLAG_DENSE) && gate)) e = fail(FBSA_EINVAL, "fbsa_bwd_dkdv: FBSA_FLAG_DENSE takes no gate");
+  if (!e && (!dk || !dv || !aligned(dk, 16) || !aligned(dv, 16)))
+    e = fail(FBSA_EINVAL, "fbsa_bwd_dkdv: dk/dv must be non-null and 16-byte aligned");
+  if (!e && sel && !aligned(sel, 4)) e = fail(FBSA_EINVAL, "fbsa_transpose_index: sel must be 4-byte aligned");
+  if (e) return e;
+  // the index (and the segment tables of long lists) depend on sel alone and run
+  // on a second stream beside dQ; dK/dV waits for both
+  const hipStream_t s = (hipStream_t)stream;
+  char *ws = (char *)workspace;
+  hipStream_t s2 = nullptr;
+  if ((e = side_stream(&s2))) return e;
+  hipEvent_t forked = nullptr, indexed = nullptr;
+  hipError_t he = hipEventCreateWithFlags(&forked, hipEventDisableTiming);
+  if (he == hipSuccess) he = hipEventCreateWithFlags(&indexed, hipEventDisableTiming);
+  if (he == hipSuccess) he = hipEventRecord(forked, s);
+  if (he == hipSuccess) he = hipStreamWaitEvent(s2, forked, 0);
+  e = hip_check(he, "fbsa_bwd: stream fork");
+  if (!e) e = run_transpose_index(d, lay, sel, ws, s2);
+  if (!e) e = run_bwd_segments(d, lay, ws, s2);
+  if (!e) e = hip_check(hipEventRecord(indexed, s2), "fbsa_bwd: hipEventRecord");
+  if (!e) e = run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, ws, s, o, lse);
+  if (!e) e = hip_check(hipStreamWaitEvent(s, indexed, 0), "fbsa_bwd: stream join");
+  if (!e) e = run_bwd_dkdv(d, lay, q, k, v, dout, gate, dk, dv, ws, s, true);
+  if (forked) (void)hipEventDestroy(forked);  // released once the streams are past them
+  if (indexed) (void)hipEventDestroy(indexed);
   return e;
 }
 

@@ -1646,13 +1646,10 @@ int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, con
   return hip_check(hipGetLastError(), "dgate_reduce_kernel launch");
 }
 
-int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
-                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s) {
-  BwdArgs a;
-  fill_bwd(d, lay, ws, a, dout);
-  a.q = q; a.k = k; a.v = v; a.sel = nullptr; a.gate = gate; a.dq = nullptr; a.dk = dk; a.dv = dv;
-  a.dgate_part = nullptr;
-  int e;
+// The segment tables of lists walked in segments (from the transposed index
+// alone): run by run_bwd_dkdv, or earlier on another stream (segments_done).
+int run_bwd_segments(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, hipStream_t s) {
+  int e = FBSA_OK;
   if (lay.seg_entries) {
     uint64_t *cnt = (uint64_t *)(ws + lay.seg_cnt), *pos = (uint64_t *)(ws + lay.seg_pos);
     hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)((lay.nwi + 1 + 255) / 256)), dim3(256), 0, s,
@@ -1666,7 +1663,21 @@ int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, c
     hipLaunchKernelGGL(seg_table_kernel, dim3((unsigned)((lay.nwi + 255) / 256)), dim3(256), 0, s,
                        (const int32_t *)(ws + lay.seg_off), (const uint64_t *)pos, lay.nwi, d->nblk, d->Hkv, d->hsel,
                        lay.seg_entries, (int32_t *)(ws + lay.wi_slot), (int4 *)(ws + lay.xtab));
-    if ((e = hip_check(hipGetLastError(), "seg_table_kernel launch"))) return e;
+    e = hip_check(hipGetLastError(), "seg_table_kernel launch");
+  }
+  return e;
+}
+
+int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
+                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s, bool segments_done) {
+  BwdArgs a;
+  fill_bwd(d, lay, ws, a, dout);
+  a.q = q; a.k = k; a.v = v; a.sel = nullptr; a.gate = gate; a.dq = nullptr; a.dk = dk; a.dv = dv;
+  a.dgate_part = nullptr;
+  int e;
+  if (!segments_done && (e = run_bwd_segments(d, lay, ws, s))) return e;
+  if (lay.seg_entries) {
+    uint64_t *pos = (uint64_t *)(ws + lay.seg_pos);
     a.wi_slot = (const int32_t *)(ws + lay.wi_slot);
     a.xtab = (const int4 *)(ws + lay.xtab);
     a.seg_tot = pos + lay.nwi;

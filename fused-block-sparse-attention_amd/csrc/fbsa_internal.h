@@ -71,7 +71,8 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 int run_bwd_dq(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
                const void *dout, const int32_t *sel, const float *gate, void *dq, float *dgate, char *ws,
                hipStream_t s, const void *o = nullptr, const float *lse = nullptr);
+int run_bwd_segments(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, hipStream_t s);
 int run_bwd_dkdv(const fbsa_attn_desc *d, const BwdLayout &lay, const void *q, const void *k, const void *v,
-                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s);
+                 const void *dout, const float *gate, void *dk, void *dv, char *ws, hipStream_t s, bool segments_done = false);
 
 }  // namespace fbsa
