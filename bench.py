@@ -613,7 +613,8 @@ def main():
                                        implementation_flop_per_launch=3.5 * flops,
                                        t_star_us=max(bflops / (PEAK_BF16_TFLOPS * 1e12),
                                                      8 * B * H * N * D * 2 / (PEAK_HBM_GBS * 1e9)) * 1e6),
-                      "stages": "prep (delta, lse), transposed index (stable radix sort), dQ, dK/dV"}
+                      "stages": ("row statistics (formed in dQ for bf16 without an output gate, else a prep pass), "
+                                 "transposed index (stable radix sort; beside dQ on a second stream), dQ, dK/dV")}
         out["ms_select_fwd_bwd"] = ms_step + t_bwd
         out["train_step_tokens_per_s"] = B * N / ((ms_step + t_bwd) * 1e-3)
 
