@@ -12,7 +12,7 @@ shape, the two kernels contend for the CUs).
 
 Prints ONE JSON line. ``value`` is tokens/s of the select+fwd step
 (BASELINE's headline); ``bwd`` times the backward of the same attention
-(prep, transposed index, dQ, dK/dV) with its own MFMA roofline (skip it with
+(row statistics, transposed index, dQ, dK/dV) with its own MFMA roofline (skip it with
 --no-bwd); ``roofline`` is the fused forward kernel (MFMA-bound: 4*B*H*nblk*kk*bs^2*D
 FLOP per launch, the reference's own formula, src/bench_crossover.py:105)
 timed with HIP events on the launch stream in separate, unoverlapped
