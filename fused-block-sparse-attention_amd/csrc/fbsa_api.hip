@@ -496,9 +496,19 @@ int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
   if (!e && sel && !aligned(sel, 4)) e = fail(FBSA_EINVAL, "fbsa_transpose_index: sel must be 4-byte aligned");
   if (e) return e;
   // the index (and the segment tables of long lists) depend on sel alone and run
-  // on a second stream beside dQ; dK/dV waits for both
+  // on a second stream beside dQ; dK/dV waits for both. Under stream capture
+  // (where creating the library's stream would be refused) they run in order
+  // on the caller's stream.
   const hipStream_t s = (hipStream_t)stream;
   char *ws = (char *)workspace;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if ((e = hip_check(hipStreamIsCapturing(s, &cap), "fbsa_bwd: hipStreamIsCapturing"))) return e;
+  if (cap != hipStreamCaptureStatusNone) {
+    e = run_transpose_index(d, lay, sel, ws, s);
+    if (!e) e = run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, ws, s, o, lse);
+    if (!e) e = run_bwd_dkdv(d, lay, q, k, v, dout, gate, dk, dv, ws, s);
+    return e;
+  }
   hipStream_t s2 = nullptr;
   if ((e = side_stream(&s2))) return e;
   hipEvent_t forked = nullptr, indexed = nullptr;
