@@ -308,8 +308,9 @@ int fbsa_bwd_dkdv(const fbsa_attn_desc *d, const void *q, const void *k, const v
  * lse (the same values, summed in the same order), so no separate pass over o
  * and dout runs, and the index stage (which reads sel alone) runs beside the
  * dQ stage on a second stream (one per host thread and device, created on
- * first use with the default priority), joined by an event before dK/dV; work
- * on `stream` after the call is ordered after all of it. Replaces _bsattn_bwd / bsattn_backward
+ * first use with the default priority), joined by an event before dK/dV (under
+ * stream capture all stages run in order on `stream`); work on `stream` after
+ * the call is ordered after all of it. Replaces _bsattn_bwd / bsattn_backward
  * (src/triton_kernel.py:77-181, 210-234) and the autograd of the gather path
  * (src/ssa_model.py:57-90). */
 int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *v, const void *o,
