@@ -229,3 +229,35 @@ def test_bench_warm_up_runs_at_least_w_steps_then_until_the_time_floor(monkeypat
     t0 = time.perf_counter()
     n = bench.warm_up(lambda: (calls.append(1), time.sleep(0.002)), 3, 0.05)
     assert time.perf_counter() - t0 >= 0.05 and n == len(calls) and n > 3
+
+
+@pytest.mark.parametrize("dtype", ["BF16", "F32"])
+def test_bwd_validates_before_launching(dtype):
+    # bf16 without an output gate (row statistics formed in dQ, the index on a
+    # second stream): fbsa_bwd checks the arguments of all four stages before it
+    # launches anything, with the stages' own messages. fp32 runs the stages in
+    # order, each checking its own arguments first: the prep stage's are checked
+    # before any launch.
+    lib = _lib.load()
+    d = _desc()
+    d.dtype = getattr(_lib, dtype)
+    nbytes = lib.fbsa_bwd_workspace_bytes(d)
+    assert nbytes > 0
+    ws = 1 << 24  # 256-byte aligned, never dereferenced
+
+    def call(n=nbytes, **kw):
+        a = dict(q=DUMMY, k=DUMMY, v=DUMMY, o=DUMMY, dout=DUMMY, lse=DUMMY, sel=DUMMY, gate=None, og=None,
+                 dq=DUMMY, dk=DUMMY, dv=DUMMY, dgate=None, dog=None)
+        a.update(kw)
+        return lib.fbsa_bwd(d, a["q"], a["k"], a["v"], a["o"], a["dout"], a["lse"], a["sel"], a["gate"], a["og"],
+                            a["dq"], a["dk"], a["dv"], a["dgate"], a["dog"], ws, n, None)
+
+    cases = [(dict(lse=None), "fbsa_bwd_prep: o/dout"), (dict(o=DUMMY + 4), "fbsa_bwd_prep: o/dout")]
+    if dtype == "BF16":
+        cases += [(dict(q=None), "fbsa_bwd_dq: null q/k/v"), (dict(dq=DUMMY + 2), "fbsa_bwd_dq: dq must"),
+                  (dict(sel=DUMMY + 2), "sel/gate/dgate must be 4-byte aligned"),
+                  (dict(dk=None), "fbsa_bwd_dkdv: dk/dv must"), (dict(dv=DUMMY + 8), "fbsa_bwd_dkdv: dk/dv must")]
+    for kw, needle in cases:
+        assert call(**kw) == _lib.EINVAL, kw
+        assert needle in lib.fbsa_last_error().decode(), (kw, lib.fbsa_last_error().decode())
+    assert call(n=nbytes - 256) == _lib.EWORKSPACE  # short of what the shape needs
