@@ -17,16 +17,19 @@ def _say(*a):
     print("[select]", *a, flush=True)
 
 
-@pytest.mark.parametrize("dtype,H", [("f32", 4), ("bf16", 4), ("f16", 4),
-                                     ("bf16", 6), ("bf16", 12), ("f16", 13),
-                                     ("f32", 1), ("bf16", 1), ("f16", 1)])
-def test_pool_mean_tok_then_heads_exact(dtype, H):
+@pytest.mark.parametrize("dtype,H,D,bs", [("f32", 4, 64, 64), ("bf16", 4, 64, 64), ("f16", 4, 64, 64),
+                                          ("bf16", 6, 64, 64), ("bf16", 12, 64, 64), ("f16", 13, 64, 64),
+                                          ("f32", 1, 64, 64), ("bf16", 1, 64, 64), ("f16", 1, 64, 64),
+                                          ("f32", 1, 256, 128), ("bf16", 1, 128, 32), ("f16", 1, 16, 16),
+                                          ("bf16", 1, 32, 128)])
+def test_pool_mean_tok_then_heads_exact(dtype, H, D, bs):
     """Mean over tokens, then over H heads. A wave takes heads w, w + 4, ... and
     loads two of them together: 6, 12 and 13 heads leave waves with an odd count.
-    One head (a plain token mean) runs one block per wave, four per workgroup."""
+    One head (a plain token mean) runs one block per wave, four per workgroup,
+    at every head dim and block size it takes."""
     from fbsa_amd import selection
     g = torch.Generator().manual_seed(0)
-    B, N, D, bs = 2, 1000, 64, 64                # N % bs != 0: zero-padded tail block
+    B, N = 2, 1000                               # N % bs != 0: zero-padded tail block
     x = randn(g, (B, H, N, D), dtype)
     _say("pool mean_tok_then_grp", dtype, H)
     got = np64(selection.pool(x.to(DEV), bs, "mean_tok_then_grp", grp=H))
