@@ -517,11 +517,21 @@ int fbsa_bwd(const fbsa_attn_desc *d, const void *q, const void *k, const void *
   if (he == hipSuccess) he = hipEventRecord(forked, s);
   if (he == hipSuccess) he = hipStreamWaitEvent(s2, forked, 0);
   e = hip_check(he, "fbsa_bwd: stream fork");
+  const bool forked_ok = !e;
   if (!e) e = run_transpose_index(d, lay, sel, ws, s2);
   if (!e) e = run_bwd_segments(d, lay, ws, s2);
-  if (!e) e = hip_check(hipEventRecord(indexed, s2), "fbsa_bwd: hipEventRecord");
+  // once s2 has been forked it is joined back into s on every path, errors
+  // included, so that no work of this call is left behind the caller's stream
+  const hipError_t re = forked_ok ? hipEventRecord(indexed, s2) : hipSuccess;
+  if (!e) e = hip_check(re, "fbsa_bwd: hipEventRecord");
   if (!e) e = run_bwd_dq(d, lay, q, k, v, dout, sel, gate, dq, dgate, ws, s, o, lse);
-  if (!e) e = hip_check(hipStreamWaitEvent(s, indexed, 0), "fbsa_bwd: stream join");
+  if (forked_ok && re == hipSuccess) {
+    const hipError_t we = hipStreamWaitEvent(s, indexed, 0);
+    if (we != hipSuccess) (void)hipStreamSynchronize(s2);
+    if (!e) e = hip_check(we, "fbsa_bwd: stream join");
+  } else if (forked_ok) {
+    (void)hipStreamSynchronize(s2);
+  }
   if (!e) e = run_bwd_dkdv(d, lay, q, k, v, dout, gate, dk, dv, ws, s, true);
   if (forked) (void)hipEventDestroy(forked);  // released once the streams are past them
   if (indexed) (void)hipEventDestroy(indexed);

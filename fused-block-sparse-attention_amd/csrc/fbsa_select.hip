@@ -261,9 +261,12 @@ __global__ __launch_bounds__(256) void pool_wave_kernel(PoolArgs a0, PoolArgs a1
   const int64_t ho = (blk / a.nblk) % a.Ho;
   const int64_t b = blk / (a.nblk * a.Ho);
   constexpr int op = OP;
-  const int64_t nval = a.l_valid - i * BS < BS ? a.l_valid - i * BS : BS;  // valid tokens in the block (>= 1)
+  // valid tokens in the block; 0 for a block wholly past l_valid (never block
+  // 0, as l_valid >= 1), whose rows then all read row i * BS - 1 and count as 0
+  const int64_t rem = a.l_valid - i * BS;
+  const int nval = rem < BS ? (rem > 0 ? (int)rem : 0) : BS;
   auto rowptr = [&](int64_t h, int t) {
-    const int tc = t < nval ? t : (int)nval - 1;
+    const int tc = t < nval ? t : nval - 1;
     return (const T *)a.x + b * a.sx[0] + h * a.sx[1] + (i * BS + tc) * a.sx[2] + 8 * c;
   };
   auto xor_sum = [&](double *v) {
@@ -413,13 +416,16 @@ __global__ __launch_bounds__(256) void pool_mean1_kernel(PoolArgs a0, PoolArgs a
   const int64_t i = blk % a.nblk;
   const int64_t ho = (blk / a.nblk) % a.Ho;
   const int64_t b = blk / (a.nblk * a.Ho);
-  const int64_t nval = a.l_valid - i * BS < BS ? a.l_valid - i * BS : BS;  // valid tokens (>= 1)
+  // valid tokens in the block; 0 for a block wholly past l_valid (never block
+  // 0, as l_valid >= 1), whose rows then all read row i * BS - 1 and count as 0
+  const int64_t rem = a.l_valid - i * BS;
+  const int nval = rem < BS ? (rem > 0 ? (int)rem : 0) : BS;
   const T *base = (const T *)a.x + b * a.sx[0] + ho * a.sx[1] + i * BS * a.sx[2] + 8 * c;
   Raw8<T> raw[RPL];
 #pragma unroll
   for (int n = 0; n < RPL; ++n) {
     const int t = tl + n * TLW;
-    const int tc = t < nval ? t : (int)nval - 1;  // rows past l_valid: a clamped address, counted as 0
+    const int tc = t < nval ? t : nval - 1;  // rows past l_valid: a clamped address, counted as 0
     raw[n] = load_raw8<T>(base + tc * a.sx[2]);
   }
   double acc[8];

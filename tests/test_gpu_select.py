@@ -37,6 +37,32 @@ def test_pool_mean_tok_then_heads_exact(dtype, H, D, bs):
     assert np.array_equal(got, ref), np.abs(got - ref).max()
 
 
+@pytest.mark.parametrize("op,H,grp,D,bs", [("mean_tok_then_grp", 2, 1, 64, 64), ("mean_tok_then_grp", 4, 4, 64, 32),
+                                           ("mean_grp_then_tok", 4, 2, 128, 128), ("minmax", 2, 1, 32, 16)])
+def test_pool_l_valid_past_whole_blocks(op, H, grp, D, bs):
+    """Tokens at positions >= l_valid count as zeros, also in blocks that lie
+    wholly past l_valid (their rows are read at the last valid row's address
+    and discarded): the result equals pooling the input with those rows zeroed."""
+    from fbsa_amd import selection
+    g = torch.Generator().manual_seed(7)
+    B, N, lv = 2, 1000, 77                       # blocks from lv // bs + 1 on hold no valid token
+    x = randn(g, (B, H, N, D), "bf16")
+    xz = x.clone()
+    xz[:, :, lv:] = 0
+    _say("pool l_valid", op, H, grp, D, bs)
+    got = selection.pool(x.to(DEV), bs, op, grp=grp, l_valid=lv)
+    if op == "minmax":
+        rmin, rmax = osel.pool_minmax(np64(xz), bs)
+        assert np.array_equal(np64(got[0]), rmin) and np.array_equal(np64(got[1]), rmax)
+        return
+    if op == "mean_tok_then_grp":
+        ref = np.concatenate([osel.pool_mean_tok_then_heads(np64(xz[:, h0:h0 + grp]), bs, "bf16")[:, None]
+                              for h0 in range(0, H, grp)], axis=1)
+    else:
+        ref = osel.pool_mean_grp_then_tok(np64(xz), H // grp, bs, "bf16")
+    assert np.array_equal(np64(got), ref), np.abs(np64(got) - ref).max()
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_pool_quest_exact(dtype):
     from fbsa_amd import selection
