@@ -4,7 +4,9 @@
 // repeatable):
 //   1. prep_kernel     per query row: delta = sum_d dO*O and lse*log2(e)
 //                      (rowstat, both stored negated so that they enter the
-//                      exponent and the dP accumulators as they are); with an
+//                      exponent and the dP accumulators as they are; for each
+//                      four rows their four lse values, then their four deltas,
+//                      so a lane holding four rows reads each as one vector); with an
 //                      output gate also dO*sigmoid(g) and
 //                      the gate gradient dO*O*(1 - sigmoid(g)).
 //   2. keys_kernel + stable radix sort (rocPRIM) + seg_off_kernel
@@ -223,10 +225,21 @@ int bwd_layout(const fbsa_attn_desc *d, BwdLayout *lay) {
 }
 
 // ----------------------------------------------------------------- stage 1
+// Row statistics (workspace and LDS): rows 4k .. 4k + 3 keep their four
+// -lse * log2 e at floats 8k .. 8k + 3 and their four -delta at 8k + 4 .. 8k + 7
+// (8 bytes a row, as a float pair would take; L is a multiple of 16, so a
+// group never spans two heads and a chunk's rows are whole groups)
+__device__ __forceinline__ int64_t rs_lse_at(int64_t row) { return (row >> 2) * 8 + (row & 3); }
+__device__ __forceinline__ int64_t rs_delta_at(int64_t row) { return (row >> 2) * 8 + 4 + (row & 3); }
+
+// row 4 k4 + r of a chunk's row statistics in LDS (the same layout)
+__device__ __forceinline__ float rs_lse(const float *M, int k4, int r) { return M[k4 * 8 + r]; }
+__device__ __forceinline__ float rs_delta(const float *M, int k4, int r) { return M[k4 * 8 + 4 + r]; }
+
 struct PrepArgs {
   const void *o, *dout, *og;
   const float *lse;
-  float2 *rowstat;
+  float *rowstat;
   void *dout_attn, *dout_gate;
   int64_t Hq, L, rows;
   int64_t so[3], sdo[3], sog[3];
@@ -326,7 +339,8 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
   if (row < a.rows && c == 0) {
     const float l = a.lse[row];
-    a.rowstat[row] = make_float2(l == -INFINITY ? -INFINITY : -l * kLog2e, -acc);  // negated: (-lse log2 e, -delta)
+    a.rowstat[rs_lse_at(row)] = l == -INFINITY ? -INFINITY : -l * kLog2e;  // negated: -lse log2 e
+    a.rowstat[rs_delta_at(row)] = -acc;                                  // and -delta
   }
 }
 
@@ -351,7 +365,7 @@ int run_bwd_prep(const fbsa_attn_desc *d, const BwdLayout &lay, const void *o, c
                  const void *out_gate, void *dout_gate, char *ws, hipStream_t s) {
   PrepArgs a;
   a.o = o; a.dout = dout; a.og = out_gate; a.lse = lse;
-  a.rowstat = (float2 *)(ws + lay.rowstat);
+  a.rowstat = (float *)(ws + lay.rowstat);
   a.dout_attn = ws + lay.dout_attn;
   a.dout_gate = dout_gate;
   a.Hq = d->Hq; a.L = d->L; a.rows = d->B * d->Hq * d->L;
@@ -448,7 +462,7 @@ int run_transpose_index(const fbsa_attn_desc *d, const BwdLayout &lay, const int
 // ----------------------------------------------------------------- stages 3, 4
 struct BwdArgs {
   const void *q, *k, *v, *dout;  // dout: gradient of the un-gated attention output
-  float2 *rowstat;  // negated (-lse * log2 e, -delta); dq_kernel replaces delta by sum P dP (16-bit types)
+  float *rowstat;  // negated -lse * log2 e and -delta by groups of four rows; dq_kernel replaces delta by sum P dP (16-bit types)
   // o, lse (bf16, no output gate; else null): dq_kernel forms the row
   // statistics itself (the prep stage is skipped) and writes both to rowstat
   const void *o;
@@ -610,7 +624,8 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
     of.load((const T *)a.o + b * a.so[0] + hq * a.so[1] + qpos * a.so[2], g);
     lraw = a.lse[(b * a.Hq + hq) * a.L + qpos];
   } else {
-    rs = a.rowstat[(b * a.Hq + hq) * a.L + qpos];
+    const int64_t row = (b * a.Hq + hq) * a.L + qpos;
+    rs = make_float2(a.rowstat[rs_lse_at(row)], a.rowstat[rs_delta_at(row)]);
   }
   __syncthreads();
   const int nv = DENSE ? (a.mask == FBSA_MASK_TOKEN_CAUSAL && i + 1 < nkb ? (int)i + 1 : nkb) : s_nvalid;
@@ -788,8 +803,9 @@ __global__ __launch_bounds__(BS * 4, (dq_minwg<T, BS, D>())) void dq_kernel(BwdA
     ddl = DINIT ? dx : dx - delta;
     const float dnew = DINIT ? delta + dx : dx;
     if (g == 0) {
-      if (fused) a.rowstat[(b * a.Hq + hq) * a.L + qpos] = make_float2(lse2 == INFINITY ? -INFINITY : -lse2, -dnew);
-      else a.rowstat[(b * a.Hq + hq) * a.L + qpos].y = -dnew;
+      const int64_t row = (b * a.Hq + hq) * a.L + qpos;
+      if (fused) a.rowstat[rs_lse_at(row)] = lse2 == INFINITY ? -INFINITY : -lse2;
+      a.rowstat[rs_delta_at(row)] = -dnew;
     }
   }
 
@@ -1010,7 +1026,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   // per-head and per-row byte steps
   const char *qh0 = (const char *)a.q + (b * a.sq[0] + (int64_t)hk * a.grp * a.sq[1]) * C::ES;
   const char *dh0 = (const char *)a.dout + (b * a.sdo[0] + (int64_t)hk * a.grp * a.sdo[1]) * C::ES;
-  const float2 *rh0 = a.rowstat + (b * a.Hq + (int64_t)hk * a.grp) * a.L;
+  const float *rh0 = a.rowstat + 2 * (b * a.Hq + (int64_t)hk * a.grp) * a.L;  // 8 bytes a row
   const int64_t qhs = a.sq[1] * C::ES, dhs = a.sdo[1] * C::ES;
   const uint32_t qrs = (uint32_t)(a.sq[2] * C::ES), drs = (uint32_t)(a.sdo[2] * C::ES);
 
@@ -1052,7 +1068,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
       // the head changes; a chunk's rows add a 32 x 32 -> 64-bit product
       // (row < L < 2^31, row strides below 4 GiB: checked by the host)
       const char *qh = qh0, *dh = dh0;
-      const float2 *rh = rh0;
+      const float *rh = rh0;
       auto issue = [&]() {
         const uint32_t row0 = (uint32_t)s_meta[ix].x * (uint32_t)BS + (uint32_t)(ic * C::KC);
         const char *qb = qh + (uint64_t)row0 * qrs;
@@ -1062,7 +1078,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         for (int n = 0; n < C::LPT; ++n) g2lds16_s(tdo[n] ? db : qb, (unsigned)toff[n], st + (n * C::NW + w) * 1024);
         // wave w copies rows w KC/NW .. (w + 1) KC/NW - 1 of the row statistics (two per lane)
         if (lane < C::KC / (2 * C::NW))
-          g2lds16(rh + row0 + w * (C::KC / C::NW) + 2 * lane, st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
+          g2lds16(rh + 2 * (row0 + w * (C::KC / C::NW)) + 4 * lane, st + 2 * C::TILE_BYTES + w * (C::KC / C::NW) * 8);
         if (++ic == C::NCH) {
           ic = 0;
           if (++ig == a.grp) {
@@ -1070,7 +1086,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
             ++ix;
             qh = qh0; dh = dh0; rh = rh0;
           } else {
-            qh += qhs; dh += dhs; rh += a.L;
+            qh += qhs; dh += dhs; rh += 2 * a.L;
           }
         }
         if (++istg == C::NSTAGE) istg = 0;
@@ -1092,7 +1108,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
         int cx = 0, cg = 0, cch = 0, cstg = 0;  // chunk c and its stage
         float x[HR / 16][4];                   // pending chunk: P (role 0) or dP (role 1)
         const char *pQ = stages, *pD = stages;
-        const float2 *pM = (const float2 *)stages;
+        const float *pM = (const float *)stages;
         for (int c = 0; c <= nchunks; ++c) {
           if (c < nchunks) {
             const int ahead = nchunks - 1 - c;
@@ -1110,7 +1126,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 const float4 pv = xs[m * XS];
                 const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
   #pragma unroll
-                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] + pM[16 * m + 4 * g + r].y);
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (x[m][r] + rs_delta(pM, 4 * m + g, r));
               }
               tr_acc(SPC, pQ, x, dvacc);  // dK^T += Q^T dS
             }
@@ -1119,7 +1135,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 
           const char *Qs = stages + cstg * C::STAGE_BYTES;
           const char *Ds = Qs + C::TILE_BYTES;
-          const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
+          const float *Ms = (const float *)(Qs + 2 * C::TILE_BYTES);
           const int4 meta = s_meta[cx];
           const int ch = cch;
           const int kind = meta.y;
@@ -1149,9 +1165,9 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
             for (int m = 0; m < HR / 16; ++m) {
   #pragma unroll
               for (int r = 0; r < 4; ++r) {
-                const float2 ms = Ms[16 * m + 4 * g + r];
+                const float ml = rs_lse(Ms, 4 * m + g, r);
                 const bool ok = kok && (16 * m + r >= tmin);
-                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
+                float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ml : ml));
                 asm volatile("" : "+v"(ev));
                 x[m][r] = ok ? ev : 0.f;
               }
@@ -1214,20 +1230,25 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
             static_for<C::KC / HR>([&](auto HC) {
               constexpr int h = decltype(HC)::value;
               constexpr int QOFF = S * C::STAGE_BYTES + h * HR * C::CPR * 16, DOFF = QOFF + C::TILE_BYTES;
-              const float2 *Mh = (const float2 *)(stages + S * C::STAGE_BYTES + 2 * C::TILE_BYTES) + h * HR;
+              const float *Mh = (const float *)(stages + S * C::STAGE_BYTES + 2 * C::TILE_BYTES) + 2 * h * HR;
               const int th = tmin - h * HR;
-              f32x4 sacc[HR / 16], dpacc[HR / 16];
-              mm_rows_frag<T, D, HR / 16, 0, QOFF>(stages, kf, sacc, g, p);   // S: query 16m+4g+r, key u
-              mm_rows_frag<T, D, HR / 16, 0, DOFF>(stages, vf, dpacc, g, p);  // dP
+              // dP accumulators start at -delta: dS = P (dP - delta) is then one product
+              f32x4 sacc[HR / 16], dpacc[HR / 16], dinit[HR / 16];
+#pragma unroll
+              for (int m = 0; m < HR / 16; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dinit[m][r] = rs_delta(Mh, 4 * m + g, r);
+              mm_rows_frag<T, D, HR / 16, 0, QOFF>(stages, kf, sacc, g, p);          // S: query 16m+4g+r, key u
+              mm_rows_frag<T, D, HR / 16, 0, DOFF>(stages, vf, dpacc, g, p, dinit);  // dP - delta
               float pp[HR / 16][4], ds[HR / 16][4];
 #pragma unroll
               for (int m = 0; m < HR / 16; ++m)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float2 ms = Mh[16 * m + 4 * g + r];  // (-lse log2 e, -delta)
-                  const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
+                  const float ml = rs_lse(Mh, 4 * m + g, r);  // -lse log2 e
+                  const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ml : ml));
                   pp[m][r] = ev;
-                  ds[m][r] = ev * (dpacc[m][r] + ms.y);
+                  ds[m][r] = ev * dpacc[m][r];
                 }
               if (kind != KIND_FULL) {
 #pragma unroll
@@ -1256,7 +1277,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
 
         const char *Qs = stages + cstg * C::STAGE_BYTES;
         const char *Ds = Qs + C::TILE_BYTES;
-        const float2 *Ms = (const float2 *)(Qs + 2 * C::TILE_BYTES);
+        const float *Ms = (const float *)(Qs + 2 * C::TILE_BYTES);
         const int4 meta = s_meta[cx];
         const int ch = cch;
         const int kind = meta.y;
@@ -1287,7 +1308,7 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
   #pragma unroll HUNROLL
         for (int h = 0; h < C::KC / HR; ++h) {
           const char *Qh = Qs + h * HR * C::CPR * 16, *Dh = Ds + h * HR * C::CPR * 16;
-          const float2 *Mh = Ms + h * HR;
+          const float *Mh = Ms + 2 * h * HR;  // 8 bytes a row
           const int th = tmin - h * HR;
           if constexpr (ROLES == 2) {
             f32x4 xacc[HR / 16];
@@ -1302,9 +1323,9 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
               for (int m = 0; m < HR / 16; ++m) {
   #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float2 ms = Mh[16 * m + 4 * g + r];
+                  const float ml = rs_lse(Mh, 4 * m + g, r);
                   const bool ok = kok && (16 * m + r >= th);
-                  float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
+                  float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[m][r], a.scale2, GC ? gt + ml : ml));
                   asm volatile("" : "+v"(ev));
                   x[m][r] = ok ? ev : 0.f;
                 }
@@ -1320,15 +1341,20 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
                 const float4 pv = xs[m * XS];
                 const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
   #pragma unroll
-                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] + Mh[16 * m + 4 * g + r].y);
+                for (int r = 0; r < 4; ++r) x[m][r] = pr[r] * (xacc[m][r] + rs_delta(Mh, 4 * m + g, r));
               }
               tr_acc(SPC, Qh, x, dvacc);  // dK^T += Q^T dS
             }
             continue;
           }
-          f32x4 sacc[HR / 16], dpacc[HR / 16];
-          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);   // S: query 16m+4g+r, key u
-          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p);  // dP
+          // dP accumulators start at -delta: dS = P (dP - delta) is then one product
+          f32x4 sacc[HR / 16], dpacc[HR / 16], dinit[HR / 16];
+  #pragma unroll
+          for (int m = 0; m < HR / 16; ++m)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) dinit[m][r] = rs_delta(Mh, 4 * m + g, r);
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Qh, kf, sacc, g, p);  // S: query 16m+4g+r, key u
+          mm_rows_frag<T, D, HR / 16, (D >= 128 ? FBSA_DKDV_WIN : 0)>(Dh, vf, dpacc, g, p, dinit);  // dP - delta
           float pp[HR / 16][4], ds[HR / 16][4];
           // every exponential is computed unconditionally; masked elements of
           // a masked chunk kind are then replaced by zeros in one uniform branch
@@ -1337,10 +1363,10 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
           for (int m = 0; m < HR / 16; ++m)
   #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const float2 ms = Mh[16 * m + 4 * g + r];
-              const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ms.x : ms.x));
+              const float ml = rs_lse(Mh, 4 * m + g, r);  // -lse log2 e
+              const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[m][r], a.scale2, GC ? gt + ml : ml));
               pp[m][r] = ev;
-              ds[m][r] = ev * (dpacc[m][r] + ms.y);
+              ds[m][r] = ev * dpacc[m][r];
             }
           if (kind != KIND_FULL) {
   #pragma unroll
@@ -1546,7 +1572,7 @@ static void fill_bwd(const fbsa_attn_desc *d, const BwdLayout &lay, char *ws, Bw
   } else {
     a.dout = dout;
   }
-  a.rowstat = (float2 *)(ws + lay.rowstat);
+  a.rowstat = (float *)(ws + lay.rowstat);
   a.seg_off = (const int32_t *)(ws + lay.seg_off);
   a.ent = (const int32_t *)(ws + lay.vals_out);
   a.scale = d->scale;
