@@ -1070,7 +1070,10 @@ __global__ __launch_bounds__((dkdv_rows<T, BS, D>() * 4), (dkdv_minwg<T, BS, D>(
       const char *qh = qh0, *dh = dh0;
       const float *rh = rh0;
       auto issue = [&]() {
-        const uint32_t row0 = (uint32_t)s_meta[ix].x * (uint32_t)BS + (uint32_t)(ic * C::KC);
+        // uniform: kept in scalar registers, so the tile and row-statistics
+        // addresses below are formed by scalar instructions
+        const uint32_t row0 =
+            (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)s_meta[ix].x * (uint32_t)BS + (uint32_t)(ic * C::KC)));
         const char *qb = qh + (uint64_t)row0 * qrs;
         const char *db = dh + (uint64_t)row0 * drs;
         char *st = stages + istg * C::STAGE_BYTES;
