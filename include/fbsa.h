@@ -16,7 +16,9 @@
  *   out_gate       (B, Hq, L, D)   strides {b, h, l} (e.g. Qwen's (B,L,Hq*D) view)
  *   sel, gate      (B, Hsel, nblk, kk) contiguous, int32 / fp32; Hsel = 1
  *                  (one selection shared by every head) or Hkv (per KV head)
- *   lse, delta     (B, Hq, L) contiguous fp32
+ *   lse            (B, Hq, L) contiguous fp32
+ *   (the backward's row statistics, delta and lse * log2 e, live in its
+ *   workspace in an internal layout; only the stage functions read them)
  *
  * The reference (apoc/fused-block-sparse-attention) is Python + Triton; the
  * entry points below replace the device work behind its Python surfaces, as
